@@ -1,0 +1,577 @@
+// Chunked causal grouped-query attention for gfx950.
+//
+// Semantics follow online_chunked_grouped_attention_mx
+// (src/ollm/backends/mlx_ops.py:32-152): scores = (q . k) * D^-1/2, key t is
+// visible to a query at absolute position p iff t <= p (causal), softmax is
+// accumulated online in fp32, out = wv / max(s, eps) in q's dtype.  Query
+// positions default to bottom-right alignment arange(Lk - Lq, Lk) (69-72).
+//
+// Three kernels:
+//   * attn_decode_split : Lq == 1.  Split-K over the key axis; each workgroup
+//     streams one key chunk of one KV head for all G = Hq/Hkv query heads
+//     (K/V read once per group), keeps per-16-lane online-softmax state in
+//     registers, merges its lanes through LDS and writes (m, s, o[D]) partials;
+//     attn_decode_merge combines the partials of all chunks.
+//   * attn_prefill_mfma : Lq > 1, D in {64, 128}, q/k/v of one dtype.
+//     Flash-style: 64-key K / V^T tiles staged in LDS, S^T = K Q^T and
+//     O^T += V^T P^T on MFMA (bf16 16x16x32, or f32 16x16x4 for fp32 inputs),
+//     so every lane owns one query row and all softmax state is in-lane.
+//     Key blocks past the causal limit of the 64-query tile are skipped.
+//   * attn_generic : any other shape (e.g. tiny head dims), one wave per query.
+#include "strata_common.h"
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <typename T>
+__device__ __forceinline__ void load_vec16(const T* p, float* out);  // 16 bytes -> floats
+
+template <>
+__device__ __forceinline__ void load_vec16<bf16_t>(const bf16_t* p, float* out) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    out[2 * c] = __uint_as_float(u[c] << 16);
+    out[2 * c + 1] = __uint_as_float(u[c] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void load_vec16<float>(const float* p, float* out) {
+  const float4 v = *reinterpret_cast<const float4*>(p);
+  out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+}
+
+// Load n (4 or 8) consecutive elements of V as floats.
+template <typename T, int N>
+__device__ __forceinline__ void load_elems(const T* p, float* out) {
+  if constexpr (sizeof(T) * N == 16) {
+    load_vec16<T>(p, out);
+  } else if constexpr (sizeof(T) == 2 && N == 4) {  // bf16 x4 = 8 bytes
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    out[0] = __uint_as_float(v.x << 16); out[1] = __uint_as_float(v.x & 0xffff0000u);
+    out[2] = __uint_as_float(v.y << 16); out[3] = __uint_as_float(v.y & 0xffff0000u);
+  } else {  // f32 x8 = 32 bytes
+    load_vec16<float>(reinterpret_cast<const float*>(p), out);
+    load_vec16<float>(reinterpret_cast<const float*>(p) + 4, out + 4);
+  }
+}
+
+// --------------------------------------------------------------- decode (Lq=1)
+// grid (nsplit, Hkv, B), block 256.  Partials layout: [B, Hq, nsplit, D + 2]
+// with (o[0..D), m, s).
+template <typename TQ, typename TK, typename TV, int D, int G>
+__global__ __launch_bounds__(256) void attn_decode_split(
+    const TQ* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
+    int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Lk,
+    int causal, int chunk, int nsplit, float scale, float eps, float* __restrict__ part,
+    TQ* __restrict__ out) {
+  constexpr int EPL = 16 / sizeof(TK);          // key elements per lane
+  constexpr int LPK = D / EPL;                  // lanes per key
+  constexpr int KPW = 64 / LPK;                 // keys per wave step
+  constexpr int J = 4;                          // keys per stream per step
+  static_assert(LPK <= 64 && 64 % LPK == 0, "unsupported head dim");
+
+  const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPK, part_idx = lane % LPK;
+  const int e0 = part_idx * EPL;
+
+  int kend = Lk;
+  if (causal) {
+    const int p = qpos ? qpos[b] : Lk - 1;
+    kend = min(Lk, p + 1);
+  }
+  const int t0 = split * chunk;
+  const int t1 = min(kend, t0 + chunk);
+
+  const TK* kb = k + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  const TV* vb = v + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+
+  float qv[G][EPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e)
+      qv[g][e] = Elem<TQ>::load(q, ((int64_t)b * Hq + hkv * G + g) * D + e0 + e);
+
+  float m[G], s[G], o[G][EPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    s[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) o[g][e] = 0.f;
+  }
+
+  // Wave-uniform loop: each step the wave covers J groups of KPW consecutive
+  // keys (KPW * D * sizeof(TK) contiguous bytes per group); the 4 waves
+  // interleave.  Stream `sub` of a wave always sees keys t == sub (mod KPW).
+  const float sl2 = scale * kLog2e;
+  for (int base = t0 + wave * KPW; base < t1; base += 4 * KPW * J) {
+    float kx[J][EPL], vx[J][EPL];
+#pragma unroll
+    for (int jj = 0; jj < J; ++jj) {
+      const int t = base + jj * 4 * KPW + sub;
+      if (t < t1) {
+        load_elems<TK, EPL>(kb + (int64_t)t * D + e0, kx[jj]);
+        load_elems<TV, EPL>(vb + (int64_t)t * D + e0, vx[jj]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) { kx[jj][e] = 0.f; vx[jj][e] = 0.f; }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float sc[J];
+      float mb = -INFINITY;
+#pragma unroll
+      for (int jj = 0; jj < J; ++jj) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) d = fmaf(qv[g][e], kx[jj][e], d);
+        d = group_sum(d, LPK);
+        sc[jj] = (base + jj * 4 * KPW + sub < t1) ? d * sl2 : -INFINITY;  // log2 domain
+        mb = fmaxf(mb, sc[jj]);
+      }
+      const float mn = fmaxf(m[g], mb);
+      if (mn != -INFINITY) {
+        const float alpha = exp2f(m[g] - mn);
+        float ps = 0.f;
+        float pj[J];
+#pragma unroll
+        for (int jj = 0; jj < J; ++jj) { pj[jj] = exp2f(sc[jj] - mn); ps += pj[jj]; }
+        s[g] = fmaf(s[g], alpha, ps);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          float acc = o[g][e] * alpha;
+#pragma unroll
+          for (int jj = 0; jj < J; ++jj) acc = fmaf(pj[jj], vx[jj][e], acc);
+          o[g][e] = acc;
+        }
+        m[g] = mn;
+      }
+    }
+  }
+
+  // ---- merge the KPW streams of each wave with shuffles, then the 4 waves in LDS
+  __shared__ float sm_m[4][G], sm_s[4][G];
+  __shared__ float sm_o[4][G][D];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mw = m[g];
+    for (int off = LPK; off < 64; off <<= 1) mw = fmaxf(mw, __shfl_xor(mw, off, 64));
+    const float f = (s[g] > 0.f) ? exp2f(m[g] - mw) : 0.f;
+    float sw = s[g] * f;
+    for (int off = LPK; off < 64; off <<= 1) sw += __shfl_xor(sw, off, 64);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float oe = o[g][e] * f;
+      for (int off = LPK; off < 64; off <<= 1) oe += __shfl_xor(oe, off, 64);
+      if (sub == 0) sm_o[wave][g][e0 + e] = oe;
+    }
+    if (lane == 0) { sm_m[wave][g] = mw; sm_s[wave][g] = sw; }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+    const int g = idx / D, d = idx - g * D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      if (sm_s[w][g] > 0.f) mx = fmaxf(mx, sm_m[w][g]);
+    float ss = 0.f, oo = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (sm_s[w][g] > 0.f) {
+        const float f = exp2f(sm_m[w][g] - mx);
+        ss = fmaf(sm_s[w][g], f, ss);
+        oo = fmaf(sm_o[w][g][d], f, oo);
+      }
+    }
+    const int hq = hkv * G + g;
+    if (nsplit == 1) {
+      Elem<TQ>::store(out, ((int64_t)b * Hq + hq) * D + d, oo / fmaxf(ss, eps));
+    } else {
+      float* pp = part + (((int64_t)b * Hq + hq) * nsplit + split) * (D + 2);
+      pp[d] = oo;
+      if (d == 0) { pp[D] = mx; pp[D + 1] = ss; }
+    }
+  }
+}
+
+// grid (B*Hq), block D.
+template <typename TQ>
+__global__ void attn_decode_merge(const float* __restrict__ part, int nsplit, int D, float eps,
+                                  TQ* __restrict__ out) {
+  const int bh = blockIdx.x;
+  const float* pp = part + (int64_t)bh * nsplit * (D + 2);
+  float mx = -INFINITY;
+  for (int i = 0; i < nsplit; ++i)
+    if (pp[i * (D + 2) + D + 1] > 0.f) mx = fmaxf(mx, pp[i * (D + 2) + D]);
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float ss = 0.f, oo = 0.f;
+    for (int i = 0; i < nsplit; ++i) {
+      const float si = pp[i * (D + 2) + D + 1];
+      if (si > 0.f) {
+        const float f = exp2f(pp[i * (D + 2) + D] - mx);
+        ss = fmaf(si, f, ss);
+        oo = fmaf(pp[i * (D + 2) + d], f, oo);
+      }
+    }
+    Elem<TQ>::store(out, (int64_t)bh * D + d, oo / fmaxf(ss, eps));
+  }
+}
+
+// ----------------------------------------------------------- prefill on MFMA
+__device__ __forceinline__ f32x4_t mfma_bf16(const bf16x8_t& a, const bf16x8_t& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mfma_f32(float a, float b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// grid (ceil(Lq/64), Hq, B), block 256: wave w owns query rows qt*64+16w..+16.
+// MFMA 16x16 layouts used (wave64, gfx950):
+//   A (16 x K): lane l holds row l%16, k-slots (l/16)*KS .. +KS
+//   B (K x 16): lane l holds col l%16, k-slots (l/16)*KS .. +KS
+//   C (16x16) : lane l holds col l%16, rows (l/16)*4 + 0..3
+// with KS = 8 for bf16 16x16x32 and KS = 1 for f32 16x16x4.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_prefill_mfma(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, int64_t kv_bs,
+    int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Hkv, int Lq, int Lk,
+    int causal, float scale, float eps, T* __restrict__ out) {
+  constexpr bool kBF16 = sizeof(T) == 2;
+  constexpr int KT = 64;                         // keys per tile
+  constexpr int KPAD = kBF16 ? 8 : 4;            // LDS row padding (elements)
+  constexpr int VPAD = kBF16 ? 8 : 4;
+  // K tile: [KT][D + KPAD]; V tile: bf16 -> transposed [D][KT + VPAD], f32 -> [KT][D + VPAD]
+  constexpr int K_ELEMS = KT * (D + KPAD);
+  constexpr int V_ELEMS = kBF16 ? D * (KT + VPAD) : KT * (D + VPAD);
+  __shared__ __attribute__((aligned(16))) T ks[K_ELEMS];
+  __shared__ __attribute__((aligned(16))) T vs[V_ELEMS];
+  __shared__ int s_kmax;
+
+  const int qt = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
+  const int G = Hq / Hkv;
+  const int hkv = hq / G;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int row = qt * 64 + wave * 16 + col;  // this lane's query row
+  const bool row_ok = row < Lq;
+  int qp = -1;
+  if (row_ok) qp = causal ? (qpos ? qpos[(int64_t)b * Lq + row] : Lk - Lq + row) : Lk - 1;
+
+  if (threadIdx.x == 0) s_kmax = 0;
+  __syncthreads();
+  if (grp == 0) atomicMax(&s_kmax, qp + 1);
+  __syncthreads();
+  const int kmax = causal ? min(Lk, s_kmax) : Lk;
+
+  const T* qrow = q + (((int64_t)b * Hq + hq) * Lq + (row_ok ? row : 0)) * D;
+  const T* kbase = k + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  const T* vbase = v + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+
+  // Q fragment as the B operand of S^T = K Q^T: col = query row, k = head dim.
+  constexpr int QF = kBF16 ? D / 32 : D / 4;
+  bf16x8_t qb[kBF16 ? QF : 1];
+  float qf[kBF16 ? 1 : QF];
+  if constexpr (kBF16) {
+#pragma unroll
+    for (int s = 0; s < QF; ++s) {
+      uint4 u = make_uint4(0, 0, 0, 0);
+      if (row_ok) u = *reinterpret_cast<const uint4*>(qrow + s * 32 + grp * 8);
+      qb[s] = __builtin_bit_cast(bf16x8_t, u);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < QF; ++s) qf[s] = row_ok ? Elem<T>::load(qrow, s * 4 + grp) : 0.f;
+  }
+
+  constexpr int DT = D / 16;  // output d tiles
+  f32x4_t acc[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  const float sl2 = scale * kLog2e;
+
+  for (int kb0 = 0; kb0 < kmax; kb0 += KT) {
+    // ---- stage K (row-major, padded) and V (bf16: transposed) tiles
+    constexpr int CH = 16 / sizeof(T);  // elements per 16-byte chunk
+    for (int c = threadIdx.x; c < KT * D / CH; c += 256) {
+      const int t = c / (D / CH), d0 = (c - t * (D / CH)) * CH;
+      const int key = kb0 + t;
+      uint4 ku = make_uint4(0, 0, 0, 0), vu = make_uint4(0, 0, 0, 0);
+      if (key < Lk) {
+        ku = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * D + d0);
+        vu = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * D + d0);
+      }
+      *reinterpret_cast<uint4*>(&ks[t * (D + KPAD) + d0]) = ku;
+      if constexpr (kBF16) {
+        const uint32_t uu[4] = {vu.x, vu.y, vu.z, vu.w};
+        uint16_t* vt = reinterpret_cast<uint16_t*>(vs);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          vt[(d0 + 2 * i) * (KT + VPAD) + t] = static_cast<uint16_t>(uu[i] & 0xffffu);
+          vt[(d0 + 2 * i + 1) * (KT + VPAD) + t] = static_cast<uint16_t>(uu[i] >> 16);
+        }
+      } else {
+        *reinterpret_cast<uint4*>(&vs[t * (D + VPAD) + d0]) = vu;
+      }
+    }
+    __syncthreads();
+
+    // ---- S^T tiles: st[j][i] = score(query row, key kb0 + 16j + 4*grp + i)
+    f32x4_t st[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f32x4_t c = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if constexpr (kBF16) {
+#pragma unroll
+        for (int s = 0; s < QF; ++s) {
+          const uint4 a = *reinterpret_cast<const uint4*>(&ks[(16 * j + col) * (D + KPAD) + s * 32 + grp * 8]);
+          c = mfma_bf16(__builtin_bit_cast(bf16x8_t, a), qb[s], c);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < QF; ++s)
+          c = mfma_f32(Elem<T>::load(ks, (16 * j + col) * (D + KPAD) + s * 4 + grp), qf[s], c);
+      }
+      st[j] = c;
+    }
+
+    // ---- online softmax (log2 domain), all state for this lane's query row
+    float mb = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kb0 + 16 * j + 4 * grp + i;
+        const bool ok = key < Lk && (!causal || key <= qp) && row_ok;
+        st[j][i] = ok ? st[j][i] * sl2 : -INFINITY;
+        mb = fmaxf(mb, st[j][i]);
+      }
+    mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+    mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+    const float mn = fmaxf(m_run, mb);
+    const float alpha = (mn == -INFINITY) ? 1.f : exp2f(m_run - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = (mn == -INFINITY) ? 0.f : exp2f(st[j][i] - mn);
+        st[j][i] = p;
+        ps += p;
+      }
+    l_run = fmaf(l_run, alpha, ps);
+    m_run = mn;
+#pragma unroll
+    for (int i = 0; i < DT; ++i) acc[i] *= alpha;
+
+    // ---- O^T += V^T P^T
+    if constexpr (kBF16) {
+      const uint16_t* vt = reinterpret_cast<const uint16_t*>(vs);
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        uint4 pu;
+        pu.x = pack_bf16x2(st[2 * c2][0], st[2 * c2][1]);
+        pu.y = pack_bf16x2(st[2 * c2][2], st[2 * c2][3]);
+        pu.z = pack_bf16x2(st[2 * c2 + 1][0], st[2 * c2 + 1][1]);
+        pu.w = pack_bf16x2(st[2 * c2 + 1][2], st[2 * c2 + 1][3]);
+        const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, pu);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const uint16_t* vr = vt + (dt * 16 + col) * (KT + VPAD);
+          const uint2 lo = *reinterpret_cast<const uint2*>(vr + 32 * c2 + 4 * grp);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 32 * c2 + 16 + 4 * grp);
+          const uint4 au = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          acc[dt] = mfma_bf16(__builtin_bit_cast(bf16x8_t, au), pb, acc[dt]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = 16 * j + 4 * grp + i;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+            acc[dt] = mfma_f32(Elem<T>::load(vs, key * (D + VPAD) + dt * 16 + col), st[j][i], acc[dt]);
+        }
+    }
+    __syncthreads();
+  }
+
+  float l_tot = l_run;
+  l_tot += __shfl_xor(l_tot, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  if (row_ok) {
+    const float inv = 1.f / fmaxf(l_tot, eps);
+    T* orow = out + (((int64_t)b * Hq + hq) * Lq + row) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Elem<T>::store(orow, dt * 16 + 4 * grp + i, acc[dt][i] * inv);
+  }
+}
+
+// ------------------------------------------------------------------ generic
+// One wave per (b, hq, query row); any D <= 256, any dtype mix.  Pass 1 finds
+// the row max and sum with lanes over keys; pass 2 has lanes over head dims.
+template <typename TQ, typename TK, typename TV>
+__global__ __launch_bounds__(64) void attn_generic(
+    const TQ* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v, int64_t kv_bs,
+    int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Hkv, int Lq, int Lk, int D,
+    int causal, float scale, float eps, TQ* __restrict__ out) {
+  const int row = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x;
+  const int hkv = hq / (Hq / Hkv);
+  __shared__ float qs[256];
+  const int64_t qoff = (((int64_t)b * Hq + hq) * Lq + row) * D;
+  for (int d = lane; d < D; d += 64) qs[d] = Elem<TQ>::load(q, qoff + d);
+  __syncthreads();
+  int kend = Lk;
+  if (causal) {
+    const int p = qpos ? qpos[(int64_t)b * Lq + row] : Lk - Lq + row;
+    kend = max(0, min(Lk, p + 1));
+  }
+  const TK* kb = k + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  const TV* vb = v + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  float m = -INFINITY, s = 0.f;
+  for (int t = lane; t < kend; t += 64) {
+    float d = 0.f;
+    for (int e = 0; e < D; ++e) d = fmaf(qs[e], Elem<TK>::load(kb, (int64_t)t * D + e), d);
+    d *= scale;
+    const float mn = fmaxf(m, d);
+    s = s * __expf(m - mn) + __expf(d - mn);
+    m = mn;
+  }
+  float mx = m;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  float sum = (s > 0.f) ? s * __expf(m - mx) : 0.f;
+  sum = wave_sum(sum);
+  for (int d0 = 0; d0 < D; d0 += 64) {
+    const int d = d0 + lane;
+    float o = 0.f;
+    if (d < D) {
+      for (int t = 0; t < kend; ++t) {
+        float sc = 0.f;
+        for (int e = 0; e < D; ++e) sc = fmaf(qs[e], Elem<TK>::load(kb, (int64_t)t * D + e), sc);
+        o = fmaf(__expf(sc * scale - mx), Elem<TV>::load(vb, (int64_t)t * D + d), o);
+      }
+      Elem<TQ>::store(out, qoff + d, o / fmaxf(sum, eps));
+    }
+  }
+}
+
+template <typename TQ, typename TK, typename TV, int D>
+int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, int64_t kv_bs,
+                  int64_t kv_hs, const int32_t* qpos, int B, int Hq, int Hkv, int Lk, int causal,
+                  float scale, float eps, void* out, hipStream_t stream) {
+  const int G = Hq / Hkv;
+  // Split the key axis so that B*Hkv*nsplit workgroups cover the GPU about 4x.
+  const int min_chunk = 256;
+  const int want = (ctx->num_cus * 4 + B * Hkv - 1) / (B * Hkv);
+  int nsplit = (Lk + min_chunk - 1) / min_chunk;
+  if (nsplit > want) nsplit = want;
+  if (nsplit < 1) nsplit = 1;
+  int chunk = (Lk + nsplit - 1) / nsplit;
+  nsplit = (Lk + chunk - 1) / chunk;
+  float* part = nullptr;
+  if (nsplit > 1) {
+    void* p = nullptr;
+    const int rc = strata_ctx_scratch(ctx, (size_t)B * Hq * nsplit * (D + 2) * sizeof(float), &p);
+    if (rc) return rc;
+    part = reinterpret_cast<float*>(p);
+  }
+  dim3 grid(nsplit, Hkv, B);
+#define STRATA_DEC(GV)                                                                        \
+  if (G == GV)                                                                                \
+    hipLaunchKernelGGL((attn_decode_split<TQ, TK, TV, D, GV>), grid, dim3(256), 0, stream,    \
+                       (const TQ*)q, (const TK*)k, (const TV*)v, kv_bs, kv_hs, qpos, Hq, Lk,  \
+                       causal, chunk, nsplit, scale, eps, part, (TQ*)out);
+  STRATA_DEC(1) else STRATA_DEC(2) else STRATA_DEC(4) else STRATA_DEC(8) else
+    return strata_set_error(STRATA_ENOTSUP, "decode attention: group size %d not in {1,2,4,8}", G);
+#undef STRATA_DEC
+  STRATA_HIP_CHECK(hipGetLastError());
+  if (nsplit > 1) {
+    hipLaunchKernelGGL((attn_decode_merge<TQ>), dim3(B * Hq), dim3(D), 0, stream, part, nsplit, D,
+                       eps, (TQ*)out);
+    STRATA_HIP_CHECK(hipGetLastError());
+  }
+  return STRATA_OK;
+}
+
+template <typename TQ, typename TK, typename TV>
+int launch_generic(const void* q, const void* k, const void* v, int64_t kv_bs, int64_t kv_hs,
+                   const int32_t* qpos, int B, int Hq, int Hkv, int Lq, int Lk, int D, int causal,
+                   float scale, float eps, void* out, hipStream_t stream) {
+  hipLaunchKernelGGL((attn_generic<TQ, TK, TV>), dim3(Lq, Hq, B), dim3(64), 0, stream,
+                     (const TQ*)q, (const TK*)k, (const TV*)v, kv_bs, kv_hs, qpos, Hq, Hkv, Lq, Lk,
+                     D, causal, scale, eps, (TQ*)out);
+  STRATA_HIP_CHECK(hipGetLastError());
+  return STRATA_OK;
+}
+
+template <typename TQ, typename TK, typename TV>
+int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v, int64_t kv_bs,
+                   int64_t kv_hs, const int32_t* qpos, int B, int Hq, int Hkv, int Lq, int Lk,
+                   int D, int causal, float scale, float eps, void* out, hipStream_t stream) {
+  const int G = Hq / Hkv;
+  const bool g_ok = G == 1 || G == 2 || G == 4 || G == 8;
+  if (Lq == 1 && g_ok && (D == 64 || D == 128)) {
+    if (D == 64)
+      return launch_decode<TQ, TK, TV, 64>(ctx, q, k, v, kv_bs, kv_hs, qpos, B, Hq, Hkv, Lk,
+                                           causal, scale, eps, out, stream);
+    return launch_decode<TQ, TK, TV, 128>(ctx, q, k, v, kv_bs, kv_hs, qpos, B, Hq, Hkv, Lk, causal,
+                                          scale, eps, out, stream);
+  }
+  if constexpr (sizeof(TQ) == sizeof(TK) && sizeof(TK) == sizeof(TV)) {
+    if (Lq > 1 && (D == 64 || D == 128)) {
+      dim3 grid((Lq + 63) / 64, Hq, B);
+      if (D == 64)
+        hipLaunchKernelGGL((attn_prefill_mfma<TQ, 64>), grid, dim3(256), 0, stream, (const TQ*)q,
+                           (const TQ*)k, (const TQ*)v, kv_bs, kv_hs, qpos, Hq, Hkv, Lq, Lk, causal,
+                           scale, eps, (TQ*)out);
+      else
+        hipLaunchKernelGGL((attn_prefill_mfma<TQ, 128>), grid, dim3(256), 0, stream, (const TQ*)q,
+                           (const TQ*)k, (const TQ*)v, kv_bs, kv_hs, qpos, Hq, Hkv, Lq, Lk, causal,
+                           scale, eps, (TQ*)out);
+      STRATA_HIP_CHECK(hipGetLastError());
+      return STRATA_OK;
+    }
+  }
+  return launch_generic<TQ, TK, TV>(q, k, v, kv_bs, kv_hs, qpos, B, Hq, Hkv, Lq, Lk, D, causal,
+                                    scale, eps, out, stream);
+}
+
+}  // namespace
+
+int strata_attention_dispatch(strata_ctx* ctx, const void* q, int qd, const void* k, int kd,
+                              const void* v, int vd, int64_t kv_bs, int64_t kv_hs,
+                              const int32_t* qpos, int B, int Hq, int Hkv, int Lq, int Lk, int D,
+                              int causal, float eps, void* out, void* stream) {
+  const float scale = 1.0f / sqrtf(static_cast<float>(D));
+  hipStream_t s = as_stream(stream);
+#define STRATA_T(c) std::conditional_t<(c) == STRATA_BF16, bf16_t, float>
+#define STRATA_CASE(A, Bc, C)                                                                  \
+  if (qd == A && kd == Bc && vd == C)                                                          \
+    return dispatch_types<STRATA_T(A), STRATA_T(Bc), STRATA_T(C)>(                             \
+        ctx, q, k, v, kv_bs, kv_hs, qpos, B, Hq, Hkv, Lq, Lk, D, causal, scale, eps, out, s);
+  STRATA_CASE(STRATA_BF16, STRATA_BF16, STRATA_BF16)
+  STRATA_CASE(STRATA_F32, STRATA_F32, STRATA_F32)
+  STRATA_CASE(STRATA_F32, STRATA_F32, STRATA_BF16)
+  STRATA_CASE(STRATA_BF16, STRATA_F32, STRATA_BF16)
+  STRATA_CASE(STRATA_F32, STRATA_BF16, STRATA_BF16)
+#undef STRATA_CASE
+#undef STRATA_T
+  return strata_set_error(STRATA_ENOTSUP, "attention: unsupported dtype combination q=%d k=%d v=%d",
+                          qd, kd, vd);
+}

@@ -1,0 +1,194 @@
+// RoPE and KV-cache append for gfx950.
+//
+// RoPE restates MLXRotaryEmbedding + apply_rotary_pos_emb_mlx / rotate_half
+// (src/ollm/llama_mlx.py:95-182): inv_freq[i] = 1/theta^(2i/D),
+// angle = fp32(fp32(pos) * inv_freq[i]), emb = [angle, angle], and
+//   out[i]       = x[i]       * cos - x[i+D/2] * sin
+//   out[i + D/2] = x[i + D/2] * cos + x[i]       * sin
+// inv_freq, cos and sin are evaluated in double and rounded once to fp32;
+// each product and the sum are rounded separately (no contraction), which
+// makes the kernel bit-identical to the build's CPU restatement.
+//
+// The KV append replaces MLXKVCache.update's concatenate
+// (src/ollm/mlx_kvcache.py:65-125) with an O(Lnew) write into a
+// preallocated [B, Hkv, Lmax, D] buffer per layer.
+#include "strata_common.h"
+
+namespace {
+
+__device__ __forceinline__ void rope_cs(int pos, int i, int D, float theta, float* c, float* s) {
+  const float inv = static_cast<float>(1.0 / pow(static_cast<double>(theta),
+                                                 static_cast<double>(2 * i) / D));
+  const float ang = __fmul_rn(static_cast<float>(pos), inv);
+  double sd, cd;
+  sincos(static_cast<double>(ang), &sd, &cd);
+  *c = static_cast<float>(cd);
+  *s = static_cast<float>(sd);
+}
+
+__device__ __forceinline__ void rotate_pair(float x1, float x2, float c, float s, float* o1,
+                                            float* o2) {
+  *o1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(-x2, s));
+  *o2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+}
+
+// In-place RoPE on x [B, H, L, D]; one thread per (b, h, l, i < D/2).
+template <typename T>
+__global__ void rope_inplace(T* __restrict__ x, const int32_t* __restrict__ pos, int B, int H,
+                             int L, int D, float theta) {
+  const int half = D / 2;
+  const int64_t total = (int64_t)B * H * L * half;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int i = idx % half;
+    const int64_t r = idx / half;  // (b*H + h)*L + l
+    const int l = r % L;
+    const int b = (r / L) / H;
+    float c, s;
+    rope_cs(pos[(int64_t)b * L + l], i, D, theta, &c, &s);
+    const int64_t off = r * D;
+    float o1, o2;
+    rotate_pair(Elem<T>::load(x, off + i), Elem<T>::load(x, off + i + half), c, s, &o1, &o2);
+    Elem<T>::store(x, off + i, o1);
+    Elem<T>::store(x, off + i + half, o2);
+  }
+}
+
+// Append src [B, H, Lnew, D] into cache [B, H, Lmax, D] at pos0 (dtype convert).
+template <typename TS, typename TC>
+__global__ void kv_copy(const TS* __restrict__ src, TC* __restrict__ dst, int B, int H, int Lnew,
+                        int Lmax, int D, int pos0) {
+  const int64_t total = (int64_t)B * H * Lnew * D;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int d = idx % D;
+    const int64_t r = idx / D;
+    const int l = r % Lnew;
+    const int64_t bh = r / Lnew;
+    Elem<TC>::store(dst, (bh * Lmax + pos0 + l) * D + d, Elem<TS>::load(src, idx));
+  }
+}
+
+// Fused: token-major projections q_src [B, L, Hq*D], k_src/v_src [B, L, Hkv*D]
+// -> q_out [B, Hq, L, D] rotated, cache K[b,h,pos0+l,:] rotated, V copied.
+// One thread per (b, l, head in Hq + 2*Hkv, i < D/2).
+template <typename TS, typename TC>
+__global__ void rope_kv_fused(const TS* __restrict__ qs, const TS* __restrict__ ks,
+                              const TS* __restrict__ vs, int B, int Hq, int Hkv, int L, int D,
+                              int Lmax, int pos0, float theta, TS* __restrict__ q_out,
+                              TC* __restrict__ kc, TC* __restrict__ vc) {
+  const int half = D / 2;
+  const int NH = Hq + 2 * Hkv;
+  const int64_t total = (int64_t)B * L * NH * half;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int i = idx % half;
+    int64_t r = idx / half;
+    const int h = r % NH;
+    r /= NH;
+    const int l = r % L;
+    const int b = r / L;
+    const int pos = pos0 + l;
+    if (h < Hq + Hkv) {
+      float c, s;
+      rope_cs(pos, i, D, theta, &c, &s);
+      float o1, o2;
+      if (h < Hq) {
+        const int64_t so = ((int64_t)b * L + l) * Hq * D + (int64_t)h * D;
+        rotate_pair(Elem<TS>::load(qs, so + i), Elem<TS>::load(qs, so + i + half), c, s, &o1, &o2);
+        const int64_t oo = (((int64_t)b * Hq + h) * L + l) * D;
+        Elem<TS>::store(q_out, oo + i, o1);
+        Elem<TS>::store(q_out, oo + i + half, o2);
+      } else {
+        const int hk = h - Hq;
+        const int64_t so = ((int64_t)b * L + l) * Hkv * D + (int64_t)hk * D;
+        // K is rotated in the source dtype first (the projection output
+        // dtype), then stored in the cache dtype.
+        rotate_pair(Elem<TS>::load(ks, so + i), Elem<TS>::load(ks, so + i + half), c, s, &o1, &o2);
+        if constexpr (sizeof(TS) == 2) {
+          o1 = bf16_to_f32(f32_to_bf16(o1));
+          o2 = bf16_to_f32(f32_to_bf16(o2));
+        }
+        const int64_t co = (((int64_t)b * Hkv + hk) * Lmax + pos) * D;
+        Elem<TC>::store(kc, co + i, o1);
+        Elem<TC>::store(kc, co + i + half, o2);
+      }
+    } else {
+      const int hv = h - Hq - Hkv;
+      const int64_t so = ((int64_t)b * L + l) * Hkv * D + (int64_t)hv * D;
+      const int64_t co = (((int64_t)b * Hkv + hv) * Lmax + pos) * D;
+      Elem<TC>::store(vc, co + i, Elem<TS>::load(vs, so + i));
+      Elem<TC>::store(vc, co + i + half, Elem<TS>::load(vs, so + i + half));
+    }
+  }
+}
+
+inline int grid_for(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return static_cast<int>(g);
+}
+
+}  // namespace
+
+int strata_rope_launch(void* q, void* k, const int32_t* pos, int B, int Hq, int Hkv, int L, int D,
+                       float theta, int dtype, void* stream) {
+  hipStream_t s = as_stream(stream);
+  struct Item { void* p; int H; } items[2] = {{q, Hq}, {k, Hkv}};
+  for (const Item& it : items) {
+    if (!it.p) continue;
+    const int64_t n = (int64_t)B * it.H * L * (D / 2);
+    if (dtype == STRATA_BF16)
+      hipLaunchKernelGGL(rope_inplace<bf16_t>, dim3(grid_for(n)), dim3(256), 0, s,
+                         reinterpret_cast<bf16_t*>(it.p), pos, B, it.H, L, D, theta);
+    else
+      hipLaunchKernelGGL(rope_inplace<float>, dim3(grid_for(n)), dim3(256), 0, s,
+                         reinterpret_cast<float*>(it.p), pos, B, it.H, L, D, theta);
+    STRATA_HIP_CHECK(hipGetLastError());
+  }
+  return STRATA_OK;
+}
+
+int strata_kv_copy_launch(const void* src, int src_dtype, void* dst, int dst_dtype, int B, int H,
+                          int Lnew, int Lmax, int D, int pos0, void* stream) {
+  hipStream_t s = as_stream(stream);
+  const int64_t n = (int64_t)B * H * Lnew * D;
+  const dim3 g(grid_for(n)), blk(256);
+  if (src_dtype == STRATA_BF16 && dst_dtype == STRATA_BF16)
+    hipLaunchKernelGGL((kv_copy<bf16_t, bf16_t>), g, blk, 0, s, (const bf16_t*)src, (bf16_t*)dst, B,
+                       H, Lnew, Lmax, D, pos0);
+  else if (src_dtype == STRATA_F32 && dst_dtype == STRATA_F32)
+    hipLaunchKernelGGL((kv_copy<float, float>), g, blk, 0, s, (const float*)src, (float*)dst, B, H,
+                       Lnew, Lmax, D, pos0);
+  else if (src_dtype == STRATA_F32 && dst_dtype == STRATA_BF16)
+    hipLaunchKernelGGL((kv_copy<float, bf16_t>), g, blk, 0, s, (const float*)src, (bf16_t*)dst, B,
+                       H, Lnew, Lmax, D, pos0);
+  else
+    hipLaunchKernelGGL((kv_copy<bf16_t, float>), g, blk, 0, s, (const bf16_t*)src, (float*)dst, B,
+                       H, Lnew, Lmax, D, pos0);
+  STRATA_HIP_CHECK(hipGetLastError());
+  return STRATA_OK;
+}
+
+int strata_rope_kv_fused_launch(const void* qs, const void* ks, const void* vs, int src_dtype,
+                                int B, int Hq, int Hkv, int L, int D, int Lmax, int pos0,
+                                float theta, void* q_out, void* kc, void* vc, int cache_dtype,
+                                void* stream) {
+  hipStream_t s = as_stream(stream);
+  const int64_t n = (int64_t)B * L * (Hq + 2 * Hkv) * (D / 2);
+  const dim3 g(grid_for(n)), blk(256);
+  if (src_dtype == STRATA_BF16 && cache_dtype == STRATA_BF16)
+    hipLaunchKernelGGL((rope_kv_fused<bf16_t, bf16_t>), g, blk, 0, s, (const bf16_t*)qs,
+                       (const bf16_t*)ks, (const bf16_t*)vs, B, Hq, Hkv, L, D, Lmax, pos0, theta,
+                       (bf16_t*)q_out, (bf16_t*)kc, (bf16_t*)vc);
+  else if (src_dtype == STRATA_F32 && cache_dtype == STRATA_F32)
+    hipLaunchKernelGGL((rope_kv_fused<float, float>), g, blk, 0, s, (const float*)qs,
+                       (const float*)ks, (const float*)vs, B, Hq, Hkv, L, D, Lmax, pos0, theta,
+                       (float*)q_out, (float*)kc, (float*)vc);
+  else
+    return strata_set_error(STRATA_ENOTSUP,
+                            "rope_kv_append: source and cache dtypes must match");
+  STRATA_HIP_CHECK(hipGetLastError());
+  return STRATA_OK;
+}

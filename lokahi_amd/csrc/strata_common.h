@@ -1,0 +1,93 @@
+// Shared device/host helpers for the Strata MI355X (gfx950) hot-path library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/strata_hip.h"
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Streaming (non-temporal) 16-byte load: weights are read exactly once.
+__device__ __forceinline__ uint4 load_nt(const uint4* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ---------------------------------------------------------------- bf16 <-> f32
+// bf16 values travel as uint16_t bit patterns (upper half of an IEEE f32).
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even, NaN kept quiet (same rule as torch / MLX casts).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Element access for the two activation dtypes the library computes with.
+struct bf16_t { uint16_t bits; };
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void store(float* p, int64_t i, float v) { p[i] = v; }
+};
+template <> struct Elem<bf16_t> {
+  static __device__ __forceinline__ float load(const bf16_t* p, int64_t i) {
+    return bf16_to_f32(p[i].bits);
+  }
+  static __device__ __forceinline__ void store(bf16_t* p, int64_t i, float v) {
+    p[i].bits = f32_to_bf16(v);
+  }
+};
+
+// ---------------------------------------------------------------- wave helpers
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float group_sum(float v, int width) {
+  for (int off = width >> 1; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------- host helpers
+// Thread-local error message; every entry point returns a status code and
+// leaves the human-readable reason here (read with strata_last_error()).
+int strata_set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+#define STRATA_HIP_CHECK(expr)                                                   \
+  do {                                                                           \
+    hipError_t _e = (expr);                                                      \
+    if (_e != hipSuccess)                                                        \
+      return strata_set_error(STRATA_EHIP, "%s failed: %s", #expr,               \
+                              hipGetErrorString(_e));                            \
+  } while (0)
+
+#define STRATA_REQUIRE(cond, ...)                                                \
+  do {                                                                           \
+    if (!(cond)) return strata_set_error(STRATA_EINVAL, __VA_ARGS__);            \
+  } while (0)
+
+struct strata_ctx {
+  int device;
+  int num_cus;
+  int max_lds_per_block;
+  void* scratch;        // device scratch arena (split-K partials), grown on demand
+  size_t scratch_bytes;
+};
+
+// Returns a device scratch buffer of at least `bytes` (owned by ctx).
+int strata_ctx_scratch(strata_ctx* ctx, size_t bytes, void** out);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

@@ -1,0 +1,39 @@
+"""Helpers shared by the GPU parity tests (host <-> device for bf16 bit arrays)."""
+import numpy as np
+import torch
+
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+
+
+def to_dev(a: np.ndarray, dev) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(dev)
+    if a.dtype == np.uint32:
+        return torch.from_numpy(a.view(np.int32)).view(torch.uint32).to(dev)
+    return torch.from_numpy(a).to(dev)
+
+
+def bf16_dev(x_f32: np.ndarray, dev) -> torch.Tensor:
+    return to_dev(f32_to_bf16_bits(x_f32), dev)
+
+
+def to_np_f32(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        return bf16_bits_to_f32(t.view(torch.int16).numpy().view(np.uint16))
+    return t.float().numpy()
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.float32:
+        return t.view(torch.int32).numpy().view(np.uint32)
+    return t.numpy()
+
+
+def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(np.asarray(got, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))

@@ -1,0 +1,130 @@
+"""q4 linear (GEMV / MFMA GEMM), bf16 linear and the quantizer vs the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import q4
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+from tests.gpu_util import bf16_dev, rel_err, to_dev, to_np_f32
+
+pytestmark = pytest.mark.gpu
+
+# Llama-3-8B decode linears (north_star config 2): (N, K)
+SHAPES_8B = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
+TOL_BF16 = 2e-2   # rel-err bound for bf16 outputs
+TOL_F32 = 1e-3    # rel-err bound for fp32 outputs
+
+
+def _problem(rng, N, K, M=1):
+    w, s, b = q4.quantize(rng.normal(0, 0.02, (N, K)).astype(np.float32), 64)
+    x = f32_to_bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
+    return w, s, b, x
+
+
+@pytest.mark.parametrize("N,K", SHAPES_8B)
+def test_gemv_decode_shapes_match_oracle(dev, N, K):
+    from lokahi_amd import ops
+    rng = np.random.default_rng(N + K)
+    w, s, b, x = _problem(rng, N, K)
+    ref = q4.quantized_matmul(bf16_bits_to_f32(x), w, s, b)
+    tw, ts, tb, tx = (to_dev(a, dev) for a in (w, s, b, x))
+    y32 = to_np_f32(ops.linear(tx, tw, ts, tb, out_dtype=torch.float32))
+    assert rel_err(y32, ref) < TOL_F32
+    y16 = to_np_f32(ops.linear(tx, tw, ts, tb))
+    assert rel_err(y16, ref) < TOL_BF16
+    # bf16 output is the RNE rounding of (nearly) the fp32 result
+    assert np.mean(f32_to_bf16_bits(y32) == f32_to_bf16_bits(y16)) > 0.999
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+def test_gemv_small_batches_and_fp32_activations(dev, M):
+    from lokahi_amd import ops
+    rng = np.random.default_rng(M)
+    N, K = 384, 1024
+    w, s, b, x = _problem(rng, N, K, M)
+    ref = q4.quantized_matmul(bf16_bits_to_f32(x), w, s, b)
+    tw, ts, tb = (to_dev(a, dev) for a in (w, s, b))
+    y = to_np_f32(ops.linear(to_dev(x, dev), tw, ts, tb, out_dtype=torch.float32))
+    assert rel_err(y, ref) < TOL_F32
+    xf = rng.normal(0, 1, (M, K)).astype(np.float32)  # reference dtype flow: fp32 activations
+    y = to_np_f32(ops.linear(torch.from_numpy(xf).to(dev), tw, ts, tb))
+    assert rel_err(y, q4.quantized_matmul(xf, w, s, b)) < TOL_F32
+
+
+def test_gemv_multi_problem_one_launch(dev):
+    from lokahi_amd import ops
+    rng = np.random.default_rng(9)
+    K = 2048
+    probs = [_problem(rng, n, K)[:3] for n in (512, 128, 128)]  # q / k / v-like
+    x = f32_to_bf16_bits(rng.normal(0, 1, (1, K)).astype(np.float32))
+    outs = ops.linear_multi(to_dev(x, dev), [tuple(to_dev(a, dev) for a in p) for p in probs],
+                            out_dtype=torch.float32)
+    for (w, s, b), y in zip(probs, outs):
+        assert rel_err(to_np_f32(y), q4.quantized_matmul(bf16_bits_to_f32(x), w, s, b)) < TOL_F32
+
+
+def test_gemv_edge_shapes(dev):
+    from lokahi_amd import ops
+    rng = np.random.default_rng(10)
+    for N, K in [(1, 64), (3, 64), (17, 192), (1000, 320)]:
+        w, s, b, x = _problem(rng, N, K)
+        y = to_np_f32(ops.linear(to_dev(x, dev), *(to_dev(a, dev) for a in (w, s, b)),
+                                 out_dtype=torch.float32))
+        assert rel_err(y, q4.quantized_matmul(bf16_bits_to_f32(x), w, s, b)) < TOL_F32, (N, K)
+    # all-zero codes: closed form y = sum_g b_g * sum x_g
+    K = 256
+    zw = np.zeros((4, K // 8), np.uint32)
+    s = f32_to_bf16_bits(np.full((4, K // 64), 0.5, np.float32))
+    bb = f32_to_bf16_bits(rng.normal(0, 1, (4, K // 64)).astype(np.float32))
+    x = f32_to_bf16_bits(rng.normal(0, 1, (1, K)).astype(np.float32))
+    y = to_np_f32(ops.linear(to_dev(x, dev), to_dev(zw, dev), to_dev(s, dev), to_dev(bb, dev),
+                             out_dtype=torch.float32))
+    expect = bf16_bits_to_f32(x).reshape(K // 64, 64).sum(1).astype(np.float64) @ bf16_bits_to_f32(bb).T
+    np.testing.assert_allclose(y[0], expect, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (200, 1000, 1024), (1000, 384, 4096),
+                                   (9, 128, 64), (2048, 4096, 4096)])
+def test_gemm_prefill_matches_oracle(dev, M, N, K):
+    from lokahi_amd import ops
+    rng = np.random.default_rng(M * 7 + N)
+    w, s, b, x = _problem(rng, N, K, M)
+    y = to_np_f32(ops.linear(to_dev(x, dev), *(to_dev(a, dev) for a in (w, s, b)),
+                             out_dtype=torch.float32))
+    ref = q4.quantized_matmul(bf16_bits_to_f32(x), w, s, b)
+    # weights are dequantized to bf16 in LDS (as MLX's qmm does): bf16 tolerance
+    assert rel_err(y, ref) < TOL_BF16
+    assert np.abs(y - ref).max() / np.abs(ref).std() < 5e-3
+
+
+def test_linear_rejects_bad_parameters(dev):
+    from lokahi_amd import ops
+    w = torch.zeros((4, 8), dtype=torch.uint32, device=dev)
+    s = torch.zeros((4, 1), dtype=torch.bfloat16, device=dev)
+    x = torch.zeros((1, 64), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        ops.linear(x, w, s, s, bits=8)
+    with pytest.raises(ValueError):
+        ops.linear(torch.zeros((1, 96), dtype=torch.bfloat16, device=dev), w, s, s)
+
+
+def test_bf16_dense_linear(dev):
+    from lokahi_amd import ops
+    rng = np.random.default_rng(12)
+    for M, N, K in [(1, 1000, 512), (3, 333, 256)]:
+        W = f32_to_bf16_bits(rng.normal(0, 0.02, (N, K)).astype(np.float32))
+        x = f32_to_bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
+        y = to_np_f32(ops.linear(to_dev(x, dev), to_dev(W, dev), None, None, out_dtype=torch.float32))
+        ref = bf16_bits_to_f32(x).astype(np.float64) @ bf16_bits_to_f32(W).T.astype(np.float64)
+        assert rel_err(y, ref) < TOL_F32
+
+
+def test_quantizer_is_bit_exact_with_oracle(dev):
+    from lokahi_amd import ops
+    rng = np.random.default_rng(13)
+    wf = rng.normal(0, 0.02, (300, 512)).astype(np.float32)
+    pw, sc, bi = ops.quantize(torch.from_numpy(wf).to(dev))
+    ew, es, eb = q4.quantize(wf, 64)
+    assert np.array_equal(pw.cpu().view(torch.int32).numpy().view(np.uint32), ew)
+    assert np.array_equal(sc.cpu().view(torch.int16).numpy().view(np.uint16), es)
+    assert np.array_equal(bi.cpu().view(torch.int16).numpy().view(np.uint16), eb)
