@@ -55,33 +55,42 @@ def gemv_roofline(iters):
     def q4(n, k):
         return ops.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02)
 
-    W = {"q": q4(4096, 4096), "k": q4(1024, 4096), "v": q4(1024, 4096),
-         "gate": q4(14336, 4096), "up": q4(14336, 4096), "down": q4(4096, 14336)}
+    # Six copies of the six-linear set (680 MB) are cycled so that no launch
+    # finds its weights in the 256 MB last-level (Infinity) cache.
+    copies = 6
+    sets = [{"q": q4(4096, 4096), "k": q4(1024, 4096), "v": q4(1024, 4096),
+             "gate": q4(14336, 4096), "up": q4(14336, 4096), "down": q4(4096, 14336)}
+            for _ in range(copies)]
     x = torch.randn((1, 4096), generator=g, device=dev).to(torch.bfloat16)
     xd = torch.randn((1, 14336), generator=g, device=dev).to(torch.bfloat16)
-    outs = {n: torch.empty((1, W[n][0].shape[0]), dtype=torch.bfloat16, device=dev) for n in W}
+    outs = {n: torch.empty((1, sets[0][n][0].shape[0]), dtype=torch.bfloat16, device=dev)
+            for n in sets[0]}
     launches = [
-        ("qkv", lambda: ops.linear_multi(x, [W["q"], W["k"], W["v"]],
-                                         outs=[outs["q"], outs["k"], outs["v"]]),
+        ("qkv", lambda W: ops.linear_multi(x, [W["q"], W["k"], W["v"]],
+                                           outs=[outs["q"], outs["k"], outs["v"]]),
          q4_bytes(4096, 4096) + 2 * q4_bytes(1024, 4096) - 2 * 2 * 4096),  # x read once
-        ("gate_up", lambda: ops.linear_multi(x, [W["gate"], W["up"]],
-                                             outs=[outs["gate"], outs["up"]]),
+        ("gate_up", lambda W: ops.linear_multi(x, [W["gate"], W["up"]],
+                                               outs=[outs["gate"], outs["up"]]),
          2 * q4_bytes(14336, 4096) - 2 * 4096),
-        ("down", lambda: ops.linear_multi(xd, [W["down"]], outs=[outs["down"]]),
+        ("down", lambda W: ops.linear_multi(xd, [W["down"]], outs=[outs["down"]]),
          q4_bytes(4096, 14336)),
     ]
     stream = torch.cuda.current_stream(dev)
     for _, fn, _ in launches:
-        for _ in range(3):
-            fn()
+        for c in range(copies):
+            fn(sets[c])
     torch.cuda.synchronize()
     per = {}
     for name, fn, nbytes in launches:
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(iters)]
-        for a, b in evs:
+        # A spin kernel holds the stream while the host enqueues every timed
+        # launch, so the event pairs bracket back-to-back kernels, not host
+        # launch latency.
+        torch.cuda._sleep(200_000_000)
+        for it, (a, b) in enumerate(evs):
             a.record(stream)
-            fn()
+            fn(sets[it % copies])
             b.record(stream)
         torch.cuda.synchronize()
         ms = sorted(a.elapsed_time(b) for a, b in evs)

@@ -219,7 +219,13 @@ int strata_attn_gqa(strata_ctx* ctx, const void* q, int q_dtype, const void* k, 
   STRATA_REQUIRE(kv_head_stride >= (int64_t)Lk * D && kv_batch_stride >= kv_head_stride * Hkv,
                  "key/value strides are smaller than the key/value extent");
   if (Lq == 0) return STRATA_OK;
-  STRATA_REQUIRE(q && k && v && out, "null tensor pointer");
+  STRATA_REQUIRE(q && out, "null tensor pointer");
+  if (Lk == 0) {  // no keys: wv = 0 and s = 0, so out = 0 / eps = 0 (mlx_ops.py:146-147)
+    STRATA_HIP_CHECK(hipMemsetAsync(out, 0, (size_t)B * Hq * Lq * D * dtype_size(q_dtype),
+                                    as_stream(stream)));
+    return STRATA_OK;
+  }
+  STRATA_REQUIRE(k && v, "null tensor pointer");
   return strata_attention_dispatch(ctx, q, q_dtype, k, k_dtype, v, v_dtype, kv_batch_stride,
                                    kv_head_stride, qpos, B, Hq, Hkv, Lq, Lk, D, causal, eps, out,
                                    stream);

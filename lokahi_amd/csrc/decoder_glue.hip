@@ -4,6 +4,10 @@
 // 647-653, 724-738; src/ollm/generation.py:42-43).
 #include "strata_common.h"
 
+// Products and sums are rounded separately (no FMA contraction) so the glue
+// matches its CPU restatement operation by operation.
+#pragma clang fp contract(off)
+
 namespace {
 
 // Block-wide sum for 256 threads.
@@ -41,7 +45,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ x,
   const float r = 1.0f / sqrtf(tot / static_cast<float>(H) + eps);
   for (int64_t i = threadIdx.x; i < H; i += 256) {
     const float v = bf16_to_f32(xr[i]);
-    yr[i] = f32_to_bf16(__fmul_rn(__fmul_rn(v, r), bf16_to_f32(w[i])));
+    yr[i] = f32_to_bf16(mul_rn(mul_rn(v, r), bf16_to_f32(w[i])));
   }
 }
 
@@ -51,7 +55,7 @@ __global__ void silu_mul_kernel(const uint16_t* __restrict__ g, const uint16_t* 
        i += (int64_t)gridDim.x * blockDim.x) {
     const float gv = bf16_to_f32(g[i]);
     const float sg = gv / (1.0f + expf(-gv));
-    a[i] = f32_to_bf16(sg * bf16_to_f32(u[i]));
+    a[i] = f32_to_bf16(mul_rn(sg, bf16_to_f32(u[i])));
   }
 }
 

@@ -14,9 +14,13 @@
 //   * every lane streams one 16-byte uint4 (32 codes) per row per step, so a
 //     wave reads 1 KiB contiguous per row per step (fully coalesced), R rows
 //     at once to keep R*16 B per lane in flight and reuse the x reads;
-//   * workgroups walk row blocks grid-stride; several linears that share x
-//     (q/k/v, gate/up) are one launch ("problems" concatenated by row).
+//   * one workgroup per row block; every lane issues all of its weight loads
+//     for a K chunk before it touches LDS, so thousands of waves keep the HBM
+//     queues full; several linears that share x (q/k/v, gate/up) are one
+//     launch ("problems" concatenated by row).
 //   * lanes reduce with xor-butterflies at the end; results are deterministic.
+#include <cstdlib>
+
 #include "strata_common.h"
 
 namespace {
@@ -65,11 +69,14 @@ __device__ __forceinline__ void stage_x(const XT* __restrict__ x, int M, int K, 
       const int mm = idx / nv, i = idx - mm * nv;
       const int m = m0 + mm;
       float sum = 0.f;
-      const uint4* xr = reinterpret_cast<const uint4*>(x) + ((int64_t)m * K + (int64_t)i * 32) / 8;
+      // rows past M read row M-1 (in bounds) and are zeroed after the loads
+      const uint4* xr = reinterpret_cast<const uint4*>(x) + ((int64_t)min(m, M - 1) * K + (int64_t)i * 32) / 8;
+      uint4 vv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vv[j] = xr[j];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (m < M) v = xr[j];
+        const uint4 v = m < M ? vv[j] : make_uint4(0, 0, 0, 0);
         uint4 pr;
         pr.x = (v.x & 0xffffu) | (v.z << 16);
         pr.y = (v.x >> 16) | (v.z & 0xffff0000u);
@@ -103,58 +110,129 @@ __device__ __forceinline__ void stage_x(const XT* __restrict__ x, int M, int K, 
   }
 }
 
-template <int R, int MT, typename XT, typename YT>
-__global__ __launch_bounds__(256) void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
-                                                      Q4Batch batch) {
+// One workgroup = NW waves, persistent over row blocks (grid-stride).  x is
+// staged into LDS once per workgroup behind the only barrier; after that each
+// wave streams its rows with no synchronization: per row block it issues all
+// R*U 16-byte weight loads (and their scales/biases, held in full 32-bit
+// registers so no load waits on another), then computes.  The wave index is
+// made wave-uniform (readfirstlane) so row/problem bookkeeping is scalar.
+// bf16 x staging split in two so its global loads can be issued before the
+// weight loads and written to LDS after them.  Thread t owns x items
+// t, t + blockDim.x (XI of them); an item is the 32 x values of one weight
+// uint4 position i of batch row mm.
+template <int MT, int XI>
+struct XStage {
+  uint4 v[XI][4];
+};
+
+template <int MT, int XI>
+__device__ __forceinline__ void xstage_load(XStage<MT, XI>& st, const uint16_t* __restrict__ x,
+                                            int M, int K, int m0, int nv) {
+#pragma unroll
+  for (int k = 0; k < XI; ++k) {
+    const int idx = min((int)(threadIdx.x + k * blockDim.x), MT * nv - 1);
+    const int mm = idx / nv, i = idx - mm * nv;
+    const int m = min(m0 + mm, M - 1);  // rows past M are zeroed at store time
+    const uint4* xr = reinterpret_cast<const uint4*>(x + (int64_t)m * K + (int64_t)i * 32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) st.v[k][j] = xr[j];
+  }
+}
+
+template <int MT, int XI>
+__device__ __forceinline__ void xstage_store(const XStage<MT, XI>& st, int M, int m0, int nv,
+                                             uint4* smem) {
+  uint4* xq = smem;
+  float* xs = reinterpret_cast<float*>(smem + MT * 4 * nv);
+#pragma unroll
+  for (int k = 0; k < XI; ++k) {
+    const int idx = threadIdx.x + k * blockDim.x;
+    if (idx >= MT * nv) break;
+    const int mm = idx / nv, i = idx - mm * nv;
+    const bool live = m0 + mm < M;
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 v = live ? st.v[k][j] : make_uint4(0, 0, 0, 0);
+      uint4 pr;
+      pr.x = (v.x & 0xffffu) | (v.z << 16);
+      pr.y = (v.x >> 16) | (v.z & 0xffff0000u);
+      pr.z = (v.y & 0xffffu) | (v.w << 16);
+      pr.w = (v.y >> 16) | (v.w & 0xffff0000u);
+      xq[(mm * 4 + j) * nv + i] = pr;
+      const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        sum += __uint_as_float(u[c] << 16) + __uint_as_float(u[c] & 0xffff0000u);
+    }
+    xs[mm * nv + i] = sum;
+  }
+}
+
+// One workgroup = NW waves = one block of NW*R rows; wave w owns R rows.
+// Order of work: x loads, then every weight/scale/bias load of the first K
+// chunk (16-byte non-temporal loads, unconditional with clamped in-bounds
+// addresses so none sits behind a branch), then x is written to LDS while the
+// weights are still in flight, one barrier, the math, the store.  XI > 0
+// selects that split staging (bf16 x); XI == 0 stages x up front (fp32 x).
+template <int NW, int R, int U, int MT, int XI, typename XT, typename YT>
+__global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
+                                                          Q4Batch batch) {
   extern __shared__ uint4 smem[];
   const int nv = K >> 5;  // uint4 (32 codes) per weight row
   const int m0 = blockIdx.y * MT;
-  stage_x<XT, MT>(x, M, K, m0, smem, nv);
-  __syncthreads();
-
-  const float* xs = reinterpret_cast<const float*>(smem + MT * (sizeof(XT) == 2 ? 4 : 8) * nv);
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int rows_per_block = 4 * R;
-  const int nrb = (batch.total_rows + rows_per_block - 1) / rows_per_block;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const float* xs = reinterpret_cast<const float*>(smem + MT * (sizeof(XT) == 2 ? 4 : 8) * nv);
 
-  for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
-    const uint4* wp[R];
-    const uint16_t* sp[R];
-    const uint16_t* bp[R];
-    int pid[R], nloc[R];
-    bool valid[R];
+  const uint4* wp[R];
+  const uint16_t* sp[R];
+  const uint16_t* bp[R];
+  int pid[R], nloc[R];
+  bool valid[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = rb * rows_per_block + wave * R + r;
-      valid[r] = row < batch.total_rows;
-      int pi = 0;
+  for (int r = 0; r < R; ++r) {
+    const int row = (blockIdx.x * NW + wave) * R + r;
+    valid[r] = row < batch.total_rows;
+    int pi = 0;
 #pragma unroll
-      for (int t = 1; t < kMaxProblems; ++t)
-        if (t < batch.count && row >= batch.p[t].row0) pi = t;
-      const int n = valid[r] ? row - batch.p[pi].row0 : 0;
-      pid[r] = pi;
-      nloc[r] = n;
-      wp[r] = batch.p[pi].w + (int64_t)n * nv;
-      sp[r] = batch.p[pi].s + (int64_t)n * (nv >> 1);
-      bp[r] = batch.p[pi].b + (int64_t)n * (nv >> 1);
-    }
+    for (int t = 1; t < kMaxProblems; ++t)
+      if (t < batch.count && row >= batch.p[t].row0) pi = t;
+    const int n = valid[r] ? row - batch.p[pi].row0 : 0;
+    pid[r] = pi;
+    nloc[r] = n;
+    wp[r] = batch.p[pi].w + (int64_t)n * nv;
+    sp[r] = batch.p[pi].s + (int64_t)n * (nv >> 1);
+    bp[r] = batch.p[pi].b + (int64_t)n * (nv >> 1);
+  }
 
-    float acc[R][MT];
+  uint4 wv[R][U];
+  uint32_t sv[R][U], bv[R][U];
+  auto issue = [&](int c0) {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int mm = 0; mm < MT; ++mm) acc[r][mm] = 0.f;
-
-    for (int i = lane; i < nv; i += 64) {
-      uint4 wv[R];
-      float sc[R], bc[R];
+    for (int u = 0; u < U; ++u) {
+      const int ic = min(c0 + lane + 64 * u, nv - 1);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        wv[r] = valid[r] ? load_nt(wp[r] + i) : make_uint4(0, 0, 0, 0);
-        sc[r] = valid[r] ? bf16_to_f32(sp[r][i >> 1]) : 0.f;
-        bc[r] = valid[r] ? bf16_to_f32(bp[r][i >> 1]) : 0.f;
+        wv[r][u] = load_nt(wp[r] + ic);
+        sv[r][u] = sp[r][ic >> 1];
+        bv[r][u] = bp[r][ic >> 1];
       }
+    }
+  };
+
+  float acc[R][MT];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) acc[r][mm] = 0.f;
+
+  auto compute = [&](int c0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // A tail lane read a valid slot; zero scale and bias remove it.
+      const bool tail = c0 + lane + 64 * u >= nv;
+      const int i = min(c0 + lane + 64 * u, nv - 1);
 #pragma unroll
       for (int mm = 0; mm < MT; ++mm) {
         const float xsum = xs[mm * nv + i];
@@ -165,7 +243,7 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(const XT* __restrict__ x, 
           for (int j = 0; j < 4; ++j) xa[j] = xq[(mm * 4 + j) * nv + i];
 #pragma unroll
           for (int r = 0; r < R; ++r) {
-            const uint32_t ww[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
+            const uint32_t ww[4] = {wv[r][u].x, wv[r][u].y, wv[r][u].z, wv[r][u].w};
             float d = 0.f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -175,8 +253,10 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(const XT* __restrict__ x, 
               d = dot2_bf16(((w >> 8) & 0x000f000fu) | kMagicPair, xa[j].z, d);
               d = dot2_bf16(((w >> 12) & 0x000f000fu) | kMagicPair, xa[j].w, d);
             }
-            acc[r][mm] = fmaf(sc[r], d, acc[r][mm]);
-            acc[r][mm] = fmaf(fmaf(-128.f, sc[r], bc[r]), xsum, acc[r][mm]);
+            const float sc = tail ? 0.f : __uint_as_float(sv[r][u] << 16);
+            const float bc = tail ? 0.f : __uint_as_float(bv[r][u] << 16);
+            acc[r][mm] = fmaf(sc, d, acc[r][mm]);
+            acc[r][mm] = fmaf(fmaf(-128.f, sc, bc), xsum, acc[r][mm]);
           }
         } else {
           const float4* xf = reinterpret_cast<const float4*>(smem);
@@ -185,7 +265,7 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(const XT* __restrict__ x, 
           for (int c = 0; c < 8; ++c) xa[c] = xf[(mm * 8 + c) * nv + i];
 #pragma unroll
           for (int r = 0; r < R; ++r) {
-            const uint32_t ww[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
+            const uint32_t ww[4] = {wv[r][u].x, wv[r][u].y, wv[r][u].z, wv[r][u].w};
             float d = 0.f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -201,119 +281,216 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(const XT* __restrict__ x, 
               d = fmaf(xa1.z, (float)(lo >> 24), d);
               d = fmaf(xa1.w, (float)(hi >> 24), d);
             }
-            acc[r][mm] = fmaf(sc[r], d, acc[r][mm]);
-            acc[r][mm] = fmaf(bc[r], xsum, acc[r][mm]);
+            const float sc = tail ? 0.f : __uint_as_float(sv[r][u] << 16);
+            const float bc = tail ? 0.f : __uint_as_float(bv[r][u] << 16);
+            acc[r][mm] = fmaf(sc, d, acc[r][mm]);
+            acc[r][mm] = fmaf(bc, xsum, acc[r][mm]);
           }
         }
       }
     }
+  };
 
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int mm = 0; mm < MT; ++mm) acc[r][mm] = wave_sum(acc[r][mm]);
-
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int mm = 0; mm < MT; ++mm) {
-        const int m = m0 + mm;
-        if (lane == r * MT + mm && valid[r] && m < M) {
-          const Q4Problem& p = batch.p[pid[r]];
-          store_y<YT>(p.y, (int64_t)m * p.n + nloc[r], acc[r][mm]);
-        }
-      }
+  if constexpr (XI > 0) {
+    XStage<MT, XI> st;
+    xstage_load<MT, XI>(st, reinterpret_cast<const uint16_t*>(x), M, K, m0, nv);
+    issue(0);
+    __builtin_amdgcn_sched_barrier(0);
+    xstage_store<MT, XI>(st, M, m0, nv, smem);
+  } else {
+    stage_x<XT, MT>(x, M, K, m0, smem, nv);
+    issue(0);
   }
+  __syncthreads();
+  compute(0);
+  for (int c0 = 64 * U; c0 < nv; c0 += 64 * U) {
+    issue(c0);
+    compute(c0);
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) acc[r][mm] = wave_sum(acc[r][mm]);
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) {
+      const int m = m0 + mm;
+      if (lane == r * MT + mm && valid[r] && m < M) {
+        const Q4Problem& p = batch.p[pid[r]];
+        store_y<YT>(p.y, (int64_t)m * p.n + nloc[r], acc[r][mm]);
+      }
+    }
 }
 
-// Dense bf16-weight GEMV (lm_head): y[m,n] = sum_k x[m,k] * W[n,k].
-template <int R, int MT, typename YT>
-__global__ __launch_bounds__(256) void bf16_gemv_kernel(const uint16_t* __restrict__ x, int M,
-                                                        int K, const uint4* __restrict__ w,
-                                                        int N, YT* __restrict__ y) {
+// Dense bf16-weight GEMV (lm_head): y[m,n] = sum_k x[m,k] * W[n,k]; same
+// load-first structure, one uint4 = 8 weights per lane per step.
+template <int NW, int R, int U, int MT, typename YT>
+__global__ __launch_bounds__(NW * 64) void bf16_gemv_kernel(const uint16_t* __restrict__ x, int M,
+                                                            int K, const uint4* __restrict__ w,
+                                                            int N, YT* __restrict__ y) {
   extern __shared__ uint4 smem[];
   const int nv = K >> 3;  // uint4 (8 bf16) per row
   const int m0 = blockIdx.y * MT;
-  for (int idx = threadIdx.x; idx < MT * nv; idx += blockDim.x) {
-    const int mm = idx / nv, i = idx - mm * nv;
-    const int m = m0 + mm;
-    smem[idx] = (m < M) ? reinterpret_cast<const uint4*>(x + (int64_t)m * K)[i]
-                        : make_uint4(0, 0, 0, 0);
-  }
-  __syncthreads();
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int nrb = (N + 4 * R - 1) / (4 * R);
-  for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
-    const int row0 = rb * 4 * R + wave * R;
-    float acc[R][MT];
+  const int row0 = (blockIdx.x * NW + wave) * R;
+  float acc[R][MT];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int mm = 0; mm < MT; ++mm) acc[r][mm] = 0.f;
-    for (int i = lane; i < nv; i += 64) {
-      uint4 wv[R];
+    for (int mm = 0; mm < MT; ++mm) acc[r][mm] = 0.f;
+  for (int c0 = 0; c0 < nv; c0 += 64 * U) {
+    uint4 wv[R][U];
 #pragma unroll
-      for (int r = 0; r < R; ++r)
-        wv[r] = (row0 + r < N) ? load_nt(w + (int64_t)(row0 + r) * nv + i)
-                               : make_uint4(0, 0, 0, 0);
+    for (int u = 0; u < U; ++u) {
+      const int i = c0 + lane + 64 * u;
+      const int ic = min(i, nv - 1);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        // unconditional, clamped load; rows past N are computed but never stored
+        const uint4 t = load_nt(w + (int64_t)min(row0 + r, N - 1) * nv + ic);
+        wv[r][u] = i < nv ? t : make_uint4(0, 0, 0, 0);
+      }
+    }
+    if (c0 == 0) {
+      for (int idx = threadIdx.x; idx < MT * nv; idx += blockDim.x) {
+        const int mm = idx / nv, i = idx - mm * nv;
+        const int m = m0 + mm;
+        smem[idx] = (m < M) ? reinterpret_cast<const uint4*>(x + (int64_t)m * K)[i]
+                            : make_uint4(0, 0, 0, 0);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = min(c0 + lane + 64 * u, nv - 1);
 #pragma unroll
       for (int mm = 0; mm < MT; ++mm) {
         const uint4 xa = smem[mm * nv + i];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           float d = acc[r][mm];
-          d = dot2_bf16(wv[r].x, xa.x, d);
-          d = dot2_bf16(wv[r].y, xa.y, d);
-          d = dot2_bf16(wv[r].z, xa.z, d);
-          d = dot2_bf16(wv[r].w, xa.w, d);
+          d = dot2_bf16(wv[r][u].x, xa.x, d);
+          d = dot2_bf16(wv[r][u].y, xa.y, d);
+          d = dot2_bf16(wv[r][u].z, xa.z, d);
+          d = dot2_bf16(wv[r][u].w, xa.w, d);
           acc[r][mm] = d;
         }
       }
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int mm = 0; mm < MT; ++mm) acc[r][mm] = wave_sum(acc[r][mm]);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int mm = 0; mm < MT; ++mm) {
-        const int m = m0 + mm;
-        if (lane == r * MT + mm && row0 + r < N && m < M)
-          Elem<YT>::store(y, (int64_t)m * N + row0 + r, acc[r][mm]);
-      }
   }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) acc[r][mm] = wave_sum(acc[r][mm]);
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) {
+      const int m = m0 + mm;
+      if (lane == r * MT + mm && row0 + r < N && m < M)
+        Elem<YT>::store(y, (int64_t)m * N + row0 + r, acc[r][mm]);
+    }
 }
 
-template <int R, int MT, typename XT, typename YT>
-int launch_q4(strata_ctx* ctx, const void* x, int M, int K, const Q4Batch& batch,
-              hipStream_t stream) {
-  const int nv = K / 32;
-  const size_t lds = (size_t)MT * nv * (sizeof(XT) == 2 ? 64 : 128) + (size_t)MT * nv * 4;
-  STRATA_REQUIRE((int64_t)lds <= ctx->max_lds_per_block,
-                 "q4 GEMV: K=%d needs %zu B of LDS per batch tile, device allows %d", K, lds,
-                 ctx->max_lds_per_block);
-  const int nrb = (batch.total_rows + 4 * R - 1) / (4 * R);
-  const int per_cu = lds <= 32768 ? 4 : (lds <= 53248 ? 3 : 2);
-  const int gx = nrb < ctx->num_cus * per_cu ? nrb : ctx->num_cus * per_cu;
-  dim3 grid(gx, (M + MT - 1) / MT);
-  hipLaunchKernelGGL((q4_gemv_kernel<R, MT, XT, YT>), grid, dim3(256), lds, stream,
-                     reinterpret_cast<const XT*>(x), M, K, batch);
-  STRATA_HIP_CHECK(hipGetLastError());
-  return STRATA_OK;
+// Launch geometry of one GEMV: waves per workgroup, rows per wave, uint4 per
+// lane per row per K chunk, batch rows per pass.
+struct GemvShape {
+  int nw, r, u, mt;
+};
+
+// Pick the geometry for `rows` output rows of `nv` uint4 each.  Aim: each
+// lane holds ~8 outstanding 16-byte weight loads (R*U ~ 8) and the launch has
+// several thousand waves; large-K rows use 8-wave workgroups so the x staged
+// in LDS is shared by more rows.
+GemvShape pick_shape(int nv, int rows, int M) {
+  // Measured on MI355X (rocprof / back-to-back launches, weights cycled past
+  // the 256 MB last-level cache): K=4096 rows prefer 4 waves x 2 rows with
+  // U=2, small launches 8 waves x 1 row; K=14336 prefers 8 waves x 1 row, U=7.
+  GemvShape g;
+  const int chunks = (nv + 63) / 64;
+  g.u = chunks <= 2 ? 2 : (chunks <= 4 ? 4 : (chunks <= 7 ? 7 : 8));
+  g.mt = M >= 4 ? 4 : (M >= 2 ? 2 : 1);
+  if (g.mt > 1) {
+    g.r = 2;
+    g.nw = 4;
+  } else if (g.u == 2) {
+    g.nw = rows < 8192 ? 8 : 4;
+    g.r = rows < 8192 ? 1 : 2;
+  } else {
+    g.nw = g.u == 4 ? 4 : 8;
+    g.r = 1;
+  }
+  if (const char* e = getenv("STRATA_GEMV_NW")) g.nw = atoi(e);
+  if (const char* e = getenv("STRATA_GEMV_R")) g.r = atoi(e);
+  if (const char* e = getenv("STRATA_GEMV_U")) g.u = atoi(e);
+  return g;
+}
+
+template <int NW, int R, int U, int MT, typename XT, typename YT>
+void launch_q4_k(const void* x, int M, int K, const Q4Batch& batch, size_t lds,
+                 hipStream_t stream) {
+  const int nwg = (batch.total_rows + NW * R - 1) / (NW * R);
+  dim3 grid(nwg, (M + MT - 1) / MT);
+  const int items = MT * (K / 32), threads = NW * 64;
+  if (sizeof(XT) == 2 && items <= threads)
+    hipLaunchKernelGGL((q4_gemv_kernel<NW, R, U, MT, 1, XT, YT>), grid, dim3(threads), lds, stream,
+                       reinterpret_cast<const XT*>(x), M, K, batch);
+  else if (sizeof(XT) == 2 && items <= 2 * threads)
+    hipLaunchKernelGGL((q4_gemv_kernel<NW, R, U, MT, 2, XT, YT>), grid, dim3(threads), lds, stream,
+                       reinterpret_cast<const XT*>(x), M, K, batch);
+  else
+    hipLaunchKernelGGL((q4_gemv_kernel<NW, R, U, MT, 0, XT, YT>), grid, dim3(threads), lds, stream,
+                       reinterpret_cast<const XT*>(x), M, K, batch);
+}
+
+template <int NW, int R, int MT, typename XT, typename YT>
+bool launch_q4_u(const GemvShape& g, const void* x, int M, int K, const Q4Batch& batch,
+                 size_t lds, hipStream_t s) {
+  switch (g.u) {
+    case 2: launch_q4_k<NW, R, 2, MT, XT, YT>(x, M, K, batch, lds, s); return true;
+    case 4: launch_q4_k<NW, R, 4, MT, XT, YT>(x, M, K, batch, lds, s); return true;
+    case 7: launch_q4_k<NW, R, 7, MT, XT, YT>(x, M, K, batch, lds, s); return true;
+    case 8: launch_q4_k<NW, R, 8, MT, XT, YT>(x, M, K, batch, lds, s); return true;
+  }
+  return false;
 }
 
 template <typename XT, typename YT>
-int dispatch_q4_m(strata_ctx* ctx, const void* x, int M, int K, const Q4Batch& batch,
-                  hipStream_t stream) {
-  // Batch tile: as many x rows per pass as LDS allows (each pass re-streams
-  // the weights, so small-M decode should fit in one pass).
-  const size_t per_row = (size_t)(K / 32) * ((sizeof(XT) == 2 ? 64 : 128) + 4);
-  const size_t cap = (size_t)ctx->max_lds_per_block;
-  if (M >= 4 && 4 * per_row <= cap) return launch_q4<2, 4, XT, YT>(ctx, x, M, K, batch, stream);
-  if (M >= 2 && 2 * per_row <= cap) return launch_q4<2, 2, XT, YT>(ctx, x, M, K, batch, stream);
-  return launch_q4<4, 1, XT, YT>(ctx, x, M, K, batch, stream);
+int dispatch_q4(strata_ctx* ctx, const void* x, int M, int K, const Q4Batch& batch,
+                hipStream_t stream) {
+  const int nv = K / 32;
+  GemvShape g = pick_shape(nv, batch.total_rows, M);
+  const size_t per_row = (size_t)nv * ((sizeof(XT) == 2 ? 64 : 128) + 4);
+  while (g.mt > 1 && g.mt * per_row > (size_t)ctx->max_lds_per_block) g.mt /= 2;
+  const size_t lds = g.mt * per_row;
+  STRATA_REQUIRE((int64_t)lds <= ctx->max_lds_per_block,
+                 "q4 GEMV: K=%d needs %zu B of LDS, device allows %d", K, lds,
+                 ctx->max_lds_per_block);
+  bool ok = false;
+  if constexpr (sizeof(XT) == 4) {
+    // fp32 activations (reference dtype flow): one geometry
+    g.u = 4;
+    if (g.mt == 4) ok = launch_q4_u<4, 2, 4, XT, YT>(g, x, M, K, batch, lds, stream);
+    else if (g.mt == 2) ok = launch_q4_u<4, 2, 2, XT, YT>(g, x, M, K, batch, lds, stream);
+    else ok = launch_q4_u<4, 2, 1, XT, YT>(g, x, M, K, batch, lds, stream);
+  } else {
+    if (g.mt == 4) ok = launch_q4_u<4, 2, 4, XT, YT>(g, x, M, K, batch, lds, stream);
+    else if (g.mt == 2) ok = launch_q4_u<4, 2, 2, XT, YT>(g, x, M, K, batch, lds, stream);
+    else if (g.nw == 4 && g.r == 4) ok = launch_q4_u<4, 4, 1, XT, YT>(g, x, M, K, batch, lds, stream);
+    else if (g.nw == 4 && g.r == 2) ok = launch_q4_u<4, 2, 1, XT, YT>(g, x, M, K, batch, lds, stream);
+    else if (g.nw == 4 && g.r == 1) ok = launch_q4_u<4, 1, 1, XT, YT>(g, x, M, K, batch, lds, stream);
+    else if (g.nw == 8 && g.r == 1) ok = launch_q4_u<8, 1, 1, XT, YT>(g, x, M, K, batch, lds, stream);
+    else if (g.nw == 8 && g.r == 2) ok = launch_q4_u<8, 2, 1, XT, YT>(g, x, M, K, batch, lds, stream);
+    else if (g.nw == 16 && g.r == 1) ok = launch_q4_u<16, 1, 1, XT, YT>(g, x, M, K, batch, lds, stream);
+  }
+  if (!ok)
+    return strata_set_error(STRATA_EINVAL, "q4 GEMV: no kernel for geometry nw=%d r=%d u=%d mt=%d",
+                            g.nw, g.r, g.u, g.mt);
+  STRATA_HIP_CHECK(hipGetLastError());
+  return STRATA_OK;
 }
 
 }  // namespace
@@ -335,37 +512,36 @@ int strata_q4_gemv(strata_ctx* ctx, const void* x, int x_dtype, int M, int K,
   batch.total_rows = rows;
   hipStream_t s = as_stream(stream);
   if (x_dtype == STRATA_BF16 && y_dtype == STRATA_BF16)
-    return dispatch_q4_m<bf16_t, bf16_t>(ctx, x, M, K, batch, s);
+    return dispatch_q4<bf16_t, bf16_t>(ctx, x, M, K, batch, s);
   if (x_dtype == STRATA_BF16 && y_dtype == STRATA_F32)
-    return dispatch_q4_m<bf16_t, float>(ctx, x, M, K, batch, s);
+    return dispatch_q4<bf16_t, float>(ctx, x, M, K, batch, s);
   if (x_dtype == STRATA_F32 && y_dtype == STRATA_F32)
-    return dispatch_q4_m<float, float>(ctx, x, M, K, batch, s);
+    return dispatch_q4<float, float>(ctx, x, M, K, batch, s);
   if (x_dtype == STRATA_F32 && y_dtype == STRATA_BF16)
-    return dispatch_q4_m<float, bf16_t>(ctx, x, M, K, batch, s);
+    return dispatch_q4<float, bf16_t>(ctx, x, M, K, batch, s);
   return strata_set_error(STRATA_EINVAL, "q4 GEMV: unsupported dtype pair (%d, %d)", x_dtype,
                           y_dtype);
 }
 
 int strata_bf16_gemv(strata_ctx* ctx, const void* x, int M, int K, const uint16_t* w, int N,
                      void* y, int y_dtype, void* stream) {
-  constexpr int R = 4;
   const int MT = M >= 4 ? 4 : (M >= 2 ? 2 : 1);
   const size_t lds = (size_t)MT * K * 2;
   STRATA_REQUIRE((int64_t)lds <= ctx->max_lds_per_block, "bf16 GEMV: K=%d too large", K);
-  const int nrb = (N + 4 * R - 1) / (4 * R);
-  const int gx = nrb < ctx->num_cus * 4 ? nrb : ctx->num_cus * 4;
-  dim3 grid(gx, (M + MT - 1) / MT);
+  // 8 uint4 (64 weights) per lane per chunk, one row per wave, 8 waves per WG.
+  constexpr int NW = 8, R = 1, U = 8;
+  dim3 grid((N + NW * R - 1) / (NW * R), (M + MT - 1) / MT);
   hipStream_t s = as_stream(stream);
   const uint16_t* xx = reinterpret_cast<const uint16_t*>(x);
   const uint4* ww = reinterpret_cast<const uint4*>(w);
-#define STRATA_BF16_LAUNCH(MTV)                                                            \
-  if (MT == MTV) {                                                                         \
-    if (y_dtype == STRATA_F32)                                                             \
-      hipLaunchKernelGGL((bf16_gemv_kernel<R, MTV, float>), grid, dim3(256), lds, s, xx, M, \
-                         K, ww, N, reinterpret_cast<float*>(y));                           \
-    else                                                                                   \
-      hipLaunchKernelGGL((bf16_gemv_kernel<R, MTV, bf16_t>), grid, dim3(256), lds, s, xx,  \
-                         M, K, ww, N, reinterpret_cast<bf16_t*>(y));                       \
+#define STRATA_BF16_LAUNCH(MTV)                                                                 \
+  if (MT == MTV) {                                                                              \
+    if (y_dtype == STRATA_F32)                                                                  \
+      hipLaunchKernelGGL((bf16_gemv_kernel<NW, R, U, MTV, float>), grid, dim3(NW * 64), lds, s, \
+                         xx, M, K, ww, N, reinterpret_cast<float*>(y));                         \
+    else                                                                                        \
+      hipLaunchKernelGGL((bf16_gemv_kernel<NW, R, U, MTV, bf16_t>), grid, dim3(NW * 64), lds,   \
+                         s, xx, M, K, ww, N, reinterpret_cast<bf16_t*>(y));                     \
   }
   STRATA_BF16_LAUNCH(1)
   STRATA_BF16_LAUNCH(2)

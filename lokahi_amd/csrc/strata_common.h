@@ -32,6 +32,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// Correctly rounded product that can never be contracted into an FMA with a
+// following add (the empty asm makes the product opaque to the optimizer).
+__device__ __forceinline__ float mul_rn(float a, float b) {
+  float p = a * b;
+  asm volatile("" : "+v"(p));
+  return p;
+}
+
 // Element access for the two activation dtypes the library computes with.
 struct bf16_t { uint16_t bits; };
 
