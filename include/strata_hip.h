@@ -188,6 +188,50 @@ int strata_quantize_q4(strata_ctx* ctx, const void* wsrc, int w_dtype, int64_t N
                        int group_size, uint32_t* w, uint16_t* scales, uint16_t* biases,
                        void* stream);
 
+
+/* ------------------------------------------------------------ decoder engine
+ * Native Llama forward + greedy generation over the kernels above.  Replaces
+ * MLXLlamaForCausalLM.__call__ (src/ollm/llama_mlx.py:863-912) with its
+ * decoder layers (608-658, 220-342, 345-432) and greedy_generate_mx
+ * (src/ollm/generation.py:7-50): prefill once, then one-token decodes whose
+ * step is captured as a HIP graph and replayed with the position and token
+ * kept on the device.  Weights and the KV cache stay caller-owned. */
+typedef struct strata_llama_config {
+  int vocab_size, hidden_size, intermediate_size, num_layers, num_heads, num_kv_heads, head_dim;
+  int group_size;
+  float rms_norm_eps, rope_theta;
+} strata_llama_config;
+
+typedef struct strata_llama_layer {
+  const uint16_t* input_norm;      /* bf16 [hidden] */
+  const uint16_t* post_norm;       /* bf16 [hidden] */
+  strata_q4_weight q, k, v, o, gate, up, down;  /* q4 triples; .y is ignored */
+} strata_llama_layer;
+
+typedef struct strata_decoder strata_decoder;
+
+/* embed / lm_head bf16 [vocab, hidden]; final_norm bf16 [hidden].  The KV
+ * cache must be bf16 with geometry (num_layers, B <= its batch, num_kv_heads,
+ * Lmax, head_dim).  max_tokens bounds B * L of one forward call. */
+int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
+                          const uint16_t* embed, const uint16_t* final_norm,
+                          const uint16_t* lm_head, const strata_llama_layer* layers,
+                          strata_kv* kv, int max_batch, int max_tokens, strata_decoder** out);
+int strata_decoder_destroy(strata_decoder* dec);
+
+/* One forward over ids int32 [B, L] (device) appended to the KV cache at its
+ * current length; writes fp32 logits of the last position, [B, vocab]. */
+int strata_decoder_forward(strata_decoder* dec, const int32_t* ids, int B, int L, float* logits,
+                           void* stream);
+
+/* Greedy generation: prefill `prompt` [B, L] (device), then max_new - 1
+ * graph-replayed decode steps; out_tokens int32 [B, max_new] (device) gets
+ * argmax(logits / temperature) of every step (ties -> lowest id).
+ * use_graph = 0 launches the decode steps from the host instead.
+ * Synchronous: returns when all tokens are written. */
+int strata_decoder_generate(strata_decoder* dec, const int32_t* prompt, int B, int L, int max_new,
+                            float temperature, int use_graph, int32_t* out_tokens, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

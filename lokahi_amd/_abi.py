@@ -38,6 +38,19 @@ class Q4Weight(C.Structure):
                 ("N", C.c_int64), ("y", C.c_void_p)]
 
 
+class LlamaConfigC(C.Structure):
+    _fields_ = [("vocab_size", C.c_int), ("hidden_size", C.c_int), ("intermediate_size", C.c_int),
+                ("num_layers", C.c_int), ("num_heads", C.c_int), ("num_kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("group_size", C.c_int), ("rms_norm_eps", C.c_float),
+                ("rope_theta", C.c_float)]
+
+
+class LlamaLayerC(C.Structure):
+    _fields_ = [("input_norm", C.c_void_p), ("post_norm", C.c_void_p), ("q", Q4Weight),
+                ("k", Q4Weight), ("v", Q4Weight), ("o", Q4Weight), ("gate", Q4Weight),
+                ("up", Q4Weight), ("down", Q4Weight)]
+
+
 _SIGS = {
     "strata_abi_version": ([], C.c_int),
     "strata_last_error": ([], C.c_char_p),
@@ -82,6 +95,14 @@ _SIGS = {
                       C.c_int),
     "strata_quantize_q4": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_int,
                             C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "strata_decoder_create": ([C.c_void_p, C.POINTER(LlamaConfigC), C.c_void_p, C.c_void_p,
+                               C.c_void_p, C.POINTER(LlamaLayerC), C.c_void_p, C.c_int, C.c_int,
+                               c_void_pp], C.c_int),
+    "strata_decoder_destroy": ([C.c_void_p], C.c_int),
+    "strata_decoder_forward": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p],
+                               C.c_int),
+    "strata_decoder_generate": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_float,
+                                 C.c_int, C.c_void_p, C.c_void_p], C.c_int),
 }
 
 EXPORTED = tuple(_SIGS.keys())

@@ -12,41 +12,10 @@
 
 #include "strata_common.h"
 
-// ---- kernel launchers (defined in the .hip translation units)
-int strata_q4_gemv(strata_ctx* ctx, const void* x, int x_dtype, int M, int K,
-                   const strata_q4_weight* ws, int count, int y_dtype, void* stream);
-int strata_bf16_gemv(strata_ctx* ctx, const void* x, int M, int K, const uint16_t* w, int N,
-                     void* y, int y_dtype, void* stream);
-int strata_q4_gemm_launch(const void* x, int M, int K, const uint32_t* w, const uint16_t* s,
-                          const uint16_t* b, int N, void* y, int y_dtype, void* stream);
-int strata_attention_dispatch(strata_ctx* ctx, const void* q, int qd, const void* k, int kd,
-                              const void* v, int vd, int64_t kv_bs, int64_t kv_hs,
-                              const int32_t* qpos, int B, int Hq, int Hkv, int Lq, int Lk, int D,
-                              int causal, float eps, void* out, void* stream);
-int strata_rope_launch(void* q, void* k, const int32_t* pos, int B, int Hq, int Hkv, int L, int D,
-                       float theta, int dtype, void* stream);
-int strata_kv_copy_launch(const void* src, int src_dtype, void* dst, int dst_dtype, int B, int H,
-                          int Lnew, int Lmax, int D, int pos0, void* stream);
-int strata_rope_kv_fused_launch(const void* qs, const void* ks, const void* vs, int src_dtype,
-                                int B, int Hq, int Hkv, int L, int D, int Lmax, int pos0,
-                                float theta, void* q_out, void* kc, void* vc, int cache_dtype,
-                                void* stream);
-int strata_rmsnorm_launch(void* x, const void* res, const uint16_t* w, int64_t rows, int64_t H,
-                          float eps, void* y, void* stream);
-int strata_silu_mul_launch(const void* g, const void* u, int64_t n, void* a, void* stream);
-int strata_add_launch(const void* x, const void* r, int64_t n, void* y, void* stream);
-int strata_embed_launch(const uint16_t* table, int64_t V, int64_t H, const int32_t* ids,
-                        int64_t n, void* y, void* stream);
-int strata_argmax_launch(const float* logits, int64_t rows, int64_t V, int32_t* out, void* stream);
-int strata_quantize_launch(const void* src, int dtype, int64_t N, int64_t K, int G, uint32_t* w,
-                           uint16_t* s, uint16_t* b, void* stream);
+#include "strata_internal.h"
 
 namespace {
 thread_local std::string g_error;
-
-bool dtype_ok(int d) { return d == STRATA_F32 || d == STRATA_BF16; }
-size_t dtype_size(int d) { return d == STRATA_F32 ? 4 : 2; }
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 }  // namespace
 
 int strata_set_error(int code, const char* fmt, ...) {
@@ -79,17 +48,25 @@ int strata_ctx_scratch(strata_ctx* ctx, size_t bytes, void** out) {
   return STRATA_OK;
 }
 
-struct strata_kv {
-  strata_ctx* ctx;
-  int layers, B, Hkv, Lmax, D, dtype;
-  void* k;
-  void* v;
-  bool owned;
-  std::vector<int> len;
-  size_t layer_elems() const { return (size_t)B * Hkv * Lmax * D; }
-  char* kl(int layer) const { return static_cast<char*>(k) + layer * layer_elems() * dtype_size(dtype); }
-  char* vl(int layer) const { return static_cast<char*>(v) + layer * layer_elems() * dtype_size(dtype); }
-};
+int strata_ctx_tickets(strata_ctx* ctx, int count, int** out) {
+  if (count > ctx->tickets_count) {
+    if (ctx->tickets) {
+      STRATA_HIP_CHECK(hipDeviceSynchronize());
+      STRATA_HIP_CHECK(hipFree(ctx->tickets));
+      ctx->tickets = nullptr;
+      ctx->tickets_count = 0;
+    }
+    const int n = count < 4096 ? 4096 : count;
+    if (hipMalloc(&ctx->tickets, (size_t)n * sizeof(int)) != hipSuccess) {
+      ctx->tickets = nullptr;
+      return strata_set_error(STRATA_ENOMEM, "ticket allocation failed");
+    }
+    STRATA_HIP_CHECK(hipMemset(ctx->tickets, 0, (size_t)n * sizeof(int)));
+    ctx->tickets_count = n;
+  }
+  *out = ctx->tickets;
+  return STRATA_OK;
+}
 
 extern "C" {
 
@@ -120,10 +97,9 @@ int strata_ctx_create(int device, strata_ctx** out) {
 
 int strata_ctx_destroy(strata_ctx* ctx) {
   if (!ctx) return STRATA_OK;
-  if (ctx->scratch) {
-    hipDeviceSynchronize();
-    hipFree(ctx->scratch);
-  }
+  hipDeviceSynchronize();
+  if (ctx->scratch) hipFree(ctx->scratch);
+  if (ctx->tickets) hipFree(ctx->tickets);
   delete ctx;
   return STRATA_OK;
 }
@@ -228,7 +204,7 @@ int strata_attn_gqa(strata_ctx* ctx, const void* q, int q_dtype, const void* k, 
   STRATA_REQUIRE(k && v, "null tensor pointer");
   return strata_attention_dispatch(ctx, q, q_dtype, k, k_dtype, v, v_dtype, kv_batch_stride,
                                    kv_head_stride, qpos, B, Hq, Hkv, Lq, Lk, D, causal, eps, out,
-                                   stream);
+                                   AttnExtra{}, stream);
 }
 
 // ---------------------------------------------------------------- KV cache
@@ -319,7 +295,7 @@ int strata_rope_kv_append(strata_kv* kv, int layer, const void* q_src, const voi
   STRATA_REQUIRE(theta > 0.f, "theta must be positive");
   if (L == 0) return STRATA_OK;
   rc = strata_rope_kv_fused_launch(q_src, k_src, v_src, src_dtype, kv->B, Hq, kv->Hkv, L, kv->D,
-                                   kv->Lmax, pos0, theta, q_out, kv->kl(layer), kv->vl(layer),
+                                   kv->Lmax, pos0, nullptr, theta, q_out, kv->kl(layer), kv->vl(layer),
                                    kv->dtype, stream);
   if (rc) return rc;
   kv->len[layer] = pos0 + L;
@@ -392,7 +368,10 @@ int strata_argmax(strata_ctx* ctx, const float* logits, int64_t rows, int64_t V,
                   void* stream) {
   STRATA_REQUIRE(ctx && logits && out && rows >= 0 && V > 0 && V <= INT32_MAX, "invalid arguments");
   if (rows == 0) return STRATA_OK;
-  return strata_argmax_launch(logits, rows, V, out, stream);
+  void* part = nullptr;
+  const int rc = strata_ctx_scratch(ctx, (size_t)rows * kArgmaxBlocks * 8, &part);
+  if (rc) return rc;
+  return strata_argmax_launch(logits, rows, V, 1.0f, out, part, stream);
 }
 
 int strata_quantize_q4(strata_ctx* ctx, const void* wsrc, int w_dtype, int64_t N, int64_t K,

@@ -7,11 +7,11 @@
 // positions default to bottom-right alignment arange(Lk - Lq, Lk) (69-72).
 //
 // Three kernels:
-//   * attn_decode_split : Lq == 1.  Split-K over the key axis; each workgroup
+//   * attn_decode_kernel : Lq == 1.  Split-K over the key axis; each workgroup
 //     streams one key chunk of one KV head for all G = Hq/Hkv query heads
 //     (K/V read once per group), keeps per-16-lane online-softmax state in
 //     registers, merges its lanes through LDS and writes (m, s, o[D]) partials;
-//     attn_decode_merge combines the partials of all chunks.
+//     the last workgroup of each KV head merges all chunks in the same launch.
 //   * attn_prefill_mfma : Lq > 1, D in {64, 128}, q/k/v of one dtype.
 //     Flash-style: 64-key K / V^T tiles staged in LDS, S^T = K Q^T and
 //     O^T += V^T P^T on MFMA (bf16 16x16x32, or f32 16x16x4 for fp32 inputs),
@@ -59,14 +59,19 @@ __device__ __forceinline__ void load_elems(const T* p, float* out) {
 }
 
 // --------------------------------------------------------------- decode (Lq=1)
-// grid (nsplit, Hkv, B), block 256.  Partials layout: [B, Hq, nsplit, D + 2]
-// with (o[0..D), m, s).
+// grid (nsplit, Hkv, B), block 256.  Each workgroup reduces one key chunk of
+// one KV head for its G query heads to (m, s, o[D]) per head.  With several
+// chunks the partials go to part [B, Hq, nsplit, D + 2] = (o[0..D), m, s);
+// the last workgroup of a (b, hkv) group to arrive (agent-scope ticket) merges
+// them and writes the output, then resets its ticket for the next launch.
+constexpr int kMaxDecodeSplits = 256;
+
 template <typename TQ, typename TK, typename TV, int D, int G>
-__global__ __launch_bounds__(256) void attn_decode_split(
+__global__ __launch_bounds__(256) void attn_decode_kernel(
     const TQ* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
-    int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Lk,
-    int causal, int chunk, int nsplit, float scale, float eps, float* __restrict__ part,
-    TQ* __restrict__ out) {
+    int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Hkv, int Lk,
+    const int* __restrict__ dlen, int causal, int chunk, int nsplit, float scale, float eps,
+    float* __restrict__ part, int* __restrict__ tickets, TQ* __restrict__ out) {
   constexpr int EPL = 16 / sizeof(TK);          // key elements per lane
   constexpr int LPK = D / EPL;                  // lanes per key
   constexpr int KPW = 64 / LPK;                 // keys per wave step
@@ -77,6 +82,9 @@ __global__ __launch_bounds__(256) void attn_decode_split(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / LPK, part_idx = lane % LPK;
   const int e0 = part_idx * EPL;
+  // A graph-replayed decode step reads the current key count from memory;
+  // chunks past it find an empty range and publish s = 0.
+  if (dlen) Lk = *dlen;
 
   int kend = Lk;
   if (causal) {
@@ -92,9 +100,7 @@ __global__ __launch_bounds__(256) void attn_decode_split(
   float qv[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < EPL; ++e)
-      qv[g][e] = Elem<TQ>::load(q, ((int64_t)b * Hq + hkv * G + g) * D + e0 + e);
+    load_elems<TQ, EPL>(q + ((int64_t)b * Hq + hkv * G + g) * D + e0, qv[g]);
 
   float m[G], s[G], o[G][EPL];
 #pragma unroll
@@ -113,14 +119,9 @@ __global__ __launch_bounds__(256) void attn_decode_split(
     float kx[J][EPL], vx[J][EPL];
 #pragma unroll
     for (int jj = 0; jj < J; ++jj) {
-      const int t = base + jj * 4 * KPW + sub;
-      if (t < t1) {
-        load_elems<TK, EPL>(kb + (int64_t)t * D + e0, kx[jj]);
-        load_elems<TV, EPL>(vb + (int64_t)t * D + e0, vx[jj]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) { kx[jj][e] = 0.f; vx[jj][e] = 0.f; }
-      }
+      const int t = min(base + jj * 4 * KPW + sub, t1 - 1);  // clamped, masked below
+      load_elems<TK, EPL>(kb + (int64_t)t * D + e0, kx[jj]);
+      load_elems<TV, EPL>(vb + (int64_t)t * D + e0, vx[jj]);
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -158,6 +159,9 @@ __global__ __launch_bounds__(256) void attn_decode_split(
   // ---- merge the KPW streams of each wave with shuffles, then the 4 waves in LDS
   __shared__ float sm_m[4][G], sm_s[4][G];
   __shared__ float sm_o[4][G][D];
+  __shared__ float sm_w[G][kMaxDecodeSplits];
+  __shared__ float sm_S[G];
+  __shared__ int sm_last;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     float mw = m[g];
@@ -198,28 +202,49 @@ __global__ __launch_bounds__(256) void attn_decode_split(
       if (d == 0) { pp[D] = mx; pp[D + 1] = ss; }
     }
   }
-}
+  if (nsplit == 1) return;
 
-// grid (B*Hq), block D.
-template <typename TQ>
-__global__ void attn_decode_merge(const float* __restrict__ part, int nsplit, int D, float eps,
-                                  TQ* __restrict__ out) {
-  const int bh = blockIdx.x;
-  const float* pp = part + (int64_t)bh * nsplit * (D + 2);
-  float mx = -INFINITY;
-  for (int i = 0; i < nsplit; ++i)
-    if (pp[i * (D + 2) + D + 1] > 0.f) mx = fmaxf(mx, pp[i * (D + 2) + D]);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float ss = 0.f, oo = 0.f;
+  // ---- cross-chunk merge by the last workgroup of this (b, hkv)
+  __threadfence();  // every thread publishes its partial stores device-wide
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int* t = tickets + b * Hkv + hkv;
+    const int prev = __hip_atomic_fetch_add(t, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == nsplit - 1;
+    if (last) __hip_atomic_store(t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm_last = last;
+  }
+  __syncthreads();
+  if (!sm_last) return;
+  __atomic_thread_fence(__ATOMIC_ACQUIRE);  // see every chunk's partials
+  const float* pb = part + ((int64_t)b * Hq + hkv * G) * nsplit * (D + 2);
+  for (int idx = threadIdx.x; idx < G * nsplit; idx += 256) {
+    const int g = idx / nsplit, i = idx - g * nsplit;
+    const float* pp = pb + ((int64_t)g * nsplit + i) * (D + 2);
+    sm_w[g][i] = pp[D + 1] > 0.f ? pp[D] : -INFINITY;   // chunk max (log2 domain)
+  }
+  __syncthreads();
+  if (threadIdx.x < G) {
+    const int g = threadIdx.x;
+    float mx = -INFINITY;
+    for (int i = 0; i < nsplit; ++i) mx = fmaxf(mx, sm_w[g][i]);
+    float ss = 0.f;
     for (int i = 0; i < nsplit; ++i) {
-      const float si = pp[i * (D + 2) + D + 1];
-      if (si > 0.f) {
-        const float f = exp2f(pp[i * (D + 2) + D] - mx);
-        ss = fmaf(si, f, ss);
-        oo = fmaf(pp[i * (D + 2) + d], f, oo);
-      }
+      const float* pp = pb + ((int64_t)g * nsplit + i) * (D + 2);
+      const float wgt = sm_w[g][i] == -INFINITY ? 0.f : exp2f(sm_w[g][i] - mx);
+      sm_w[g][i] = wgt;
+      ss = fmaf(pp[D + 1], wgt, ss);
     }
-    Elem<TQ>::store(out, (int64_t)bh * D + d, oo / fmaxf(ss, eps));
+    sm_S[g] = ss;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+    const int g = idx / D, d = idx - g * D;
+    const float* pp = pb + (int64_t)g * nsplit * (D + 2) + d;
+    float oo = 0.f;
+#pragma unroll 8
+    for (int i = 0; i < nsplit; ++i) oo = fmaf(pp[(int64_t)i * (D + 2)], sm_w[g][i], oo);
+    Elem<TQ>::store(out, ((int64_t)b * Hq + hkv * G + g) * D + d, oo / fmaxf(sm_S[g], eps));
   }
 }
 
@@ -245,7 +270,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_prefill_mfma(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, int64_t kv_bs,
     int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Hkv, int Lq, int Lk,
-    int causal, float scale, float eps, T* __restrict__ out) {
+    int causal, float scale, float eps, int out_tm, T* __restrict__ out) {
   constexpr bool kBF16 = sizeof(T) == 2;
   constexpr int KT = 64;                         // keys per tile
   constexpr int KPAD = kBF16 ? 8 : 4;            // LDS row padding (elements)
@@ -413,7 +438,9 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
   l_tot += __shfl_xor(l_tot, 32, 64);
   if (row_ok) {
     const float inv = 1.f / fmaxf(l_tot, eps);
-    T* orow = out + (((int64_t)b * Hq + hq) * Lq + row) * D;
+    // out_tm: token-major [B, Lq, Hq, D] (the o_proj input); else [B, Hq, Lq, D]
+    T* orow = out + (out_tm ? (((int64_t)b * Lq + row) * Hq + hq) * D
+                            : (((int64_t)b * Hq + hq) * Lq + row) * D);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -471,41 +498,59 @@ __global__ __launch_bounds__(64) void attn_generic(
   }
 }
 
+// Key-axis split of the decode kernel for `Lcap` keys: enough workgroups to
+// cover the GPU about 4x, at least 64 keys (one 4-wave sweep) per split, at
+// most kMaxDecodeSplits splits.
+void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
+  const int min_chunk = 64;
+  int want = (num_cus * 4 + B * Hkv - 1) / (B * Hkv);
+  if (want > kMaxDecodeSplits) want = kMaxDecodeSplits;
+  int nsplit = (Lcap + min_chunk - 1) / min_chunk;
+  if (nsplit > want) nsplit = want;
+  if (nsplit < 1) nsplit = 1;
+  int chunk = (Lcap + nsplit - 1) / nsplit;
+  if (chunk < 1) chunk = 1;
+  nsplit = (Lcap + chunk - 1) / chunk;
+  if (nsplit < 1) nsplit = 1;
+  *nsplit_out = nsplit;
+  *chunk_out = chunk;
+}
+
 template <typename TQ, typename TK, typename TV, int D>
 int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, int64_t kv_bs,
                   int64_t kv_hs, const int32_t* qpos, int B, int Hq, int Hkv, int Lk, int causal,
-                  float scale, float eps, void* out, hipStream_t stream) {
+                  float scale, float eps, void* out, const AttnExtra& ex, hipStream_t stream) {
   const int G = Hq / Hkv;
-  // Split the key axis so that B*Hkv*nsplit workgroups cover the GPU about 4x.
-  const int min_chunk = 256;
-  const int want = (ctx->num_cus * 4 + B * Hkv - 1) / (B * Hkv);
-  int nsplit = (Lk + min_chunk - 1) / min_chunk;
-  if (nsplit > want) nsplit = want;
-  if (nsplit < 1) nsplit = 1;
-  int chunk = (Lk + nsplit - 1) / nsplit;
-  nsplit = (Lk + chunk - 1) / chunk;
+  int nsplit, chunk;
+  decode_split_geometry(ctx->num_cus, B, Hkv, Lk, &nsplit, &chunk);
   float* part = nullptr;
+  int* tickets = nullptr;
   if (nsplit > 1) {
-    void* p = nullptr;
-    const int rc = strata_ctx_scratch(ctx, (size_t)B * Hq * nsplit * (D + 2) * sizeof(float), &p);
-    if (rc) return rc;
-    part = reinterpret_cast<float*>(p);
+    if (ex.part) {  // decoder-owned partials and tickets (graph-safe)
+      if (ex.part_splits < nsplit || !ex.tickets)
+        return strata_set_error(STRATA_EINVAL, "decode attention: partials buffer too small");
+      part = ex.part;
+      tickets = ex.tickets;
+    } else {
+      void* p = nullptr;
+      const int rc = strata_ctx_scratch(ctx, (size_t)B * Hq * nsplit * (D + 2) * sizeof(float), &p);
+      if (rc) return rc;
+      part = reinterpret_cast<float*>(p);
+      const int rt = strata_ctx_tickets(ctx, B * Hkv, &tickets);
+      if (rt) return rt;
+    }
   }
   dim3 grid(nsplit, Hkv, B);
 #define STRATA_DEC(GV)                                                                        \
   if (G == GV)                                                                                \
-    hipLaunchKernelGGL((attn_decode_split<TQ, TK, TV, D, GV>), grid, dim3(256), 0, stream,    \
-                       (const TQ*)q, (const TK*)k, (const TV*)v, kv_bs, kv_hs, qpos, Hq, Lk,  \
-                       causal, chunk, nsplit, scale, eps, part, (TQ*)out);
+    hipLaunchKernelGGL((attn_decode_kernel<TQ, TK, TV, D, GV>), grid, dim3(256), 0, stream,   \
+                       (const TQ*)q, (const TK*)k, (const TV*)v, kv_bs, kv_hs, qpos, Hq, Hkv, \
+                       Lk, ex.dlen, causal, chunk, nsplit, scale, eps, part, tickets,         \
+                       (TQ*)out);
   STRATA_DEC(1) else STRATA_DEC(2) else STRATA_DEC(4) else STRATA_DEC(8) else
     return strata_set_error(STRATA_ENOTSUP, "decode attention: group size %d not in {1,2,4,8}", G);
 #undef STRATA_DEC
   STRATA_HIP_CHECK(hipGetLastError());
-  if (nsplit > 1) {
-    hipLaunchKernelGGL((attn_decode_merge<TQ>), dim3(B * Hq), dim3(D), 0, stream, part, nsplit, D,
-                       eps, (TQ*)out);
-    STRATA_HIP_CHECK(hipGetLastError());
-  }
   return STRATA_OK;
 }
 
@@ -523,15 +568,16 @@ int launch_generic(const void* q, const void* k, const void* v, int64_t kv_bs, i
 template <typename TQ, typename TK, typename TV>
 int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v, int64_t kv_bs,
                    int64_t kv_hs, const int32_t* qpos, int B, int Hq, int Hkv, int Lq, int Lk,
-                   int D, int causal, float scale, float eps, void* out, hipStream_t stream) {
+                   int D, int causal, float scale, float eps, void* out, const AttnExtra& ex,
+                   hipStream_t stream) {
   const int G = Hq / Hkv;
   const bool g_ok = G == 1 || G == 2 || G == 4 || G == 8;
   if (Lq == 1 && g_ok && (D == 64 || D == 128)) {
     if (D == 64)
       return launch_decode<TQ, TK, TV, 64>(ctx, q, k, v, kv_bs, kv_hs, qpos, B, Hq, Hkv, Lk,
-                                           causal, scale, eps, out, stream);
+                                           causal, scale, eps, out, ex, stream);
     return launch_decode<TQ, TK, TV, 128>(ctx, q, k, v, kv_bs, kv_hs, qpos, B, Hq, Hkv, Lk, causal,
-                                          scale, eps, out, stream);
+                                          scale, eps, out, ex, stream);
   }
   if constexpr (sizeof(TQ) == sizeof(TK) && sizeof(TK) == sizeof(TV)) {
     if (Lq > 1 && (D == 64 || D == 128)) {
@@ -539,11 +585,11 @@ int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v,
       if (D == 64)
         hipLaunchKernelGGL((attn_prefill_mfma<TQ, 64>), grid, dim3(256), 0, stream, (const TQ*)q,
                            (const TQ*)k, (const TQ*)v, kv_bs, kv_hs, qpos, Hq, Hkv, Lq, Lk, causal,
-                           scale, eps, (TQ*)out);
+                           scale, eps, ex.out_tm, (TQ*)out);
       else
         hipLaunchKernelGGL((attn_prefill_mfma<TQ, 128>), grid, dim3(256), 0, stream, (const TQ*)q,
                            (const TQ*)k, (const TQ*)v, kv_bs, kv_hs, qpos, Hq, Hkv, Lq, Lk, causal,
-                           scale, eps, (TQ*)out);
+                           scale, eps, ex.out_tm, (TQ*)out);
       STRATA_HIP_CHECK(hipGetLastError());
       return STRATA_OK;
     }
@@ -554,17 +600,24 @@ int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v,
 
 }  // namespace
 
+int strata_attn_decode_splits(strata_ctx* ctx, int B, int Hkv, int Lcap) {
+  int nsplit, chunk;
+  decode_split_geometry(ctx->num_cus, B, Hkv, Lcap, &nsplit, &chunk);
+  return nsplit;
+}
+
 int strata_attention_dispatch(strata_ctx* ctx, const void* q, int qd, const void* k, int kd,
                               const void* v, int vd, int64_t kv_bs, int64_t kv_hs,
                               const int32_t* qpos, int B, int Hq, int Hkv, int Lq, int Lk, int D,
-                              int causal, float eps, void* out, void* stream) {
+                              int causal, float eps, void* out, const AttnExtra& ex,
+                              void* stream) {
   const float scale = 1.0f / sqrtf(static_cast<float>(D));
   hipStream_t s = as_stream(stream);
 #define STRATA_T(c) std::conditional_t<(c) == STRATA_BF16, bf16_t, float>
 #define STRATA_CASE(A, Bc, C)                                                                  \
   if (qd == A && kd == Bc && vd == C)                                                          \
     return dispatch_types<STRATA_T(A), STRATA_T(Bc), STRATA_T(C)>(                             \
-        ctx, q, k, v, kv_bs, kv_hs, qpos, B, Hq, Hkv, Lq, Lk, D, causal, scale, eps, out, s);
+        ctx, q, k, v, kv_bs, kv_hs, qpos, B, Hq, Hkv, Lq, Lk, D, causal, scale, eps, out, ex, s);
   STRATA_CASE(STRATA_BF16, STRATA_BF16, STRATA_BF16)
   STRATA_CASE(STRATA_F32, STRATA_F32, STRATA_F32)
   STRATA_CASE(STRATA_F32, STRATA_F32, STRATA_BF16)

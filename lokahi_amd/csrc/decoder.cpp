@@ -1,0 +1,344 @@
+// Native Llama decoder engine: forward passes and greedy generation launched
+// from C++ over the library's kernels, with the decode step captured once as
+// a HIP graph and replayed per token.
+//
+// Follows MLXLlamaForCausalLM.__call__ (src/ollm/llama_mlx.py:863-912),
+// MLXLlamaModel.__call__ (740-833), MLXLlamaDecoderLayer.__call__ (608-658),
+// MLXLlamaAttention.__call__ (220-342), MLXLlamaMLP (345-432) and
+// greedy_generate_mx (src/ollm/generation.py:7-50).  Per layer:
+//   h <- h + delta;  xn = RMSNorm(h)               (fused residual + norm)
+//   q, k, v = q4(xn)                               (one launch)
+//   RoPE(q, k) at the cache position; append k, v   (one launch)
+//   a = GQA attention(q, K[:len], V[:len])          (split-K decode / MFMA prefill)
+//   h <- h + q4_o(a);  xn = RMSNorm(h)
+//   delta = q4_down(silu(q4_gate(xn)) * q4_up(xn))  (gate/up in one launch)
+// then logits = lm_head(RMSNorm(h + delta)) for the last position, argmax.
+// Device counters {step, position, key count} let one captured step serve
+// every token: RoPE/append read the position, attention reads the key count,
+// and a final one-thread kernel records the token and advances the counters.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <vector>
+
+#include "strata_internal.h"
+
+struct strata_decoder {
+  strata_ctx* ctx;
+  strata_llama_config cfg;
+  const uint16_t* embed;
+  const uint16_t* final_norm;
+  const uint16_t* lm_head;
+  std::vector<strata_llama_layer> layers;
+  strata_kv* kv;
+  int max_batch, max_tokens;
+  // activations (bf16 unless noted)
+  void *h, *xn, *q, *k, *v, *qr, *attn, *o, *gate, *up, *act, *delta, *hn;
+  float* logits;          // fp32 [max_batch, vocab]
+  int32_t* ids;           // [max_batch] current input ids of a decode step
+  int* counters;          // {step, position, key count}
+  float* part;            // split-K partials for graph-mode decode attention
+  int part_splits;
+  int* tickets;           // split-K merge tickets [B * Hkv], zeroed once
+  void* amax;             // argmax partials [max_batch * kArgmaxBlocks * 8 B]
+  hipStream_t stream;     // the decoder's own stream (graph capture / replay)
+  hipGraphExec_t graph;   // captured decode step
+  int graph_batch;
+  float graph_temp;
+  int32_t* graph_out;
+  int graph_out_stride;
+};
+
+namespace {
+
+int alloc(void** p, size_t bytes) {
+  if (hipMalloc(p, bytes) != hipSuccess) {
+    *p = nullptr;
+    return strata_set_error(STRATA_ENOMEM, "decoder: allocation of %zu bytes failed", bytes);
+  }
+  return STRATA_OK;
+}
+
+#define RC(expr)                \
+  do {                          \
+    const int _rc = (expr);     \
+    if (_rc) return _rc;        \
+  } while (0)
+
+// One decoder forward over T = B*L tokens at positions pos0..pos0+L-1
+// (pos0 < 0: read from counters[1], decode graph mode, L == 1).
+int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream) {
+  const strata_llama_config& c = d->cfg;
+  const int T = B * L;
+  const int H = c.hidden_size, F = c.intermediate_size, D = c.head_dim;
+  const int Hq = c.num_heads, Hkv = c.num_kv_heads;
+  strata_kv* kv = d->kv;
+  const int64_t kv_bs = (int64_t)Hkv * kv->Lmax * D, kv_hs = (int64_t)kv->Lmax * D;
+  const bool graph_mode = pos0 < 0;
+  for (int li = 0; li < c.num_layers; ++li) {
+    const strata_llama_layer& Lw = d->layers[li];
+    RC(strata_rmsnorm_launch(d->h, li == 0 ? nullptr : d->delta, Lw.input_norm, T, H,
+                             c.rms_norm_eps, d->xn, stream));
+    strata_q4_weight qkv[3] = {Lw.q, Lw.k, Lw.v};
+    qkv[0].y = d->q;
+    qkv[1].y = d->k;
+    qkv[2].y = d->v;
+    if (T <= 8) {
+      RC(strata_q4_gemv(d->ctx, d->xn, STRATA_BF16, T, H, qkv, 3, STRATA_BF16, stream));
+    } else {
+      for (auto& w : qkv)
+        RC(strata_q4_gemm_launch(d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
+                                 stream));
+    }
+    void* kc = kv->kl(li);
+    void* vc = kv->vl(li);
+    RC(strata_rope_kv_fused_launch(d->q, d->k, d->v, STRATA_BF16, B, Hq, Hkv, L, D, kv->Lmax,
+                                   graph_mode ? 0 : pos0, graph_mode ? d->counters + 1 : nullptr,
+                                   c.rope_theta, d->qr, kc, vc, STRATA_BF16, stream));
+    AttnExtra ex;
+    if (graph_mode) {
+      ex.dlen = d->counters + 2;
+      ex.part = d->part;
+      ex.part_splits = d->part_splits;
+      ex.tickets = d->tickets;
+      RC(strata_attention_dispatch(d->ctx, d->qr, STRATA_BF16, kc, STRATA_BF16, vc, STRATA_BF16,
+                                   kv_bs, kv_hs, nullptr, B, Hq, Hkv, 1, kv->Lmax, D, 1, 1e-12f,
+                                   d->attn, ex, stream));
+    } else {
+      ex.out_tm = 1;  // prefill writes [B, L, Hq, D], the o_proj input layout
+      RC(strata_attention_dispatch(d->ctx, d->qr, STRATA_BF16, kc, STRATA_BF16, vc, STRATA_BF16,
+                                   kv_bs, kv_hs, nullptr, B, Hq, Hkv, L, pos0 + L, D, 1, 1e-12f,
+                                   d->attn, ex, stream));
+    }
+    strata_q4_weight o = Lw.o;
+    o.y = d->o;
+    if (T <= 8) RC(strata_q4_gemv(d->ctx, d->attn, STRATA_BF16, T, Hq * D, &o, 1, STRATA_BF16, stream));
+    else RC(strata_q4_gemm_launch(d->attn, T, Hq * D, o.w, o.scales, o.biases, (int)o.N, o.y,
+                                  STRATA_BF16, stream));
+    RC(strata_rmsnorm_launch(d->h, d->o, Lw.post_norm, T, H, c.rms_norm_eps, d->xn, stream));
+    strata_q4_weight gu[2] = {Lw.gate, Lw.up};
+    gu[0].y = d->gate;
+    gu[1].y = d->up;
+    if (T <= 8) {
+      RC(strata_q4_gemv(d->ctx, d->xn, STRATA_BF16, T, H, gu, 2, STRATA_BF16, stream));
+    } else {
+      for (auto& w : gu)
+        RC(strata_q4_gemm_launch(d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
+                                 stream));
+    }
+    RC(strata_silu_mul_launch(d->gate, d->up, (int64_t)T * F, d->act, stream));
+    strata_q4_weight dn = Lw.down;
+    dn.y = d->delta;
+    if (T <= 8) RC(strata_q4_gemv(d->ctx, d->act, STRATA_BF16, T, F, &dn, 1, STRATA_BF16, stream));
+    else RC(strata_q4_gemm_launch(d->act, T, F, dn.w, dn.scales, dn.biases, (int)dn.N, dn.y,
+                                  STRATA_BF16, stream));
+  }
+  // final norm of h + delta, then lm_head on the last position of each row
+  RC(strata_rmsnorm_launch(d->h, d->delta, d->final_norm, T, H, c.rms_norm_eps, d->hn, stream));
+  if (L == 1) {
+    RC(strata_bf16_gemv(d->ctx, d->hn, B, H, d->lm_head, c.vocab_size, d->logits, STRATA_F32,
+                        stream));
+  } else {
+    for (int b = 0; b < B; ++b)
+      RC(strata_bf16_gemv(d->ctx, static_cast<char*>(d->hn) + ((int64_t)b * L + L - 1) * H * 2, 1,
+                          H, d->lm_head, c.vocab_size, d->logits + (int64_t)b * c.vocab_size,
+                          STRATA_F32, stream));
+  }
+  return STRATA_OK;
+}
+
+int check_forward(strata_decoder* d, int B, int L) {
+  STRATA_REQUIRE(d != nullptr, "decoder is NULL");
+  STRATA_REQUIRE(B >= 1 && B <= d->max_batch && B <= d->kv->B,
+                 "batch %d exceeds the decoder/KV-cache batch", B);
+  STRATA_REQUIRE(L >= 1 && (int64_t)B * L <= d->max_tokens,
+                 "B*L = %lld exceeds max_tokens %d", (long long)B * L, d->max_tokens);
+  STRATA_REQUIRE(d->kv->B == B, "KV cache batch %d differs from input batch %d", d->kv->B, B);
+  const int pos0 = d->kv->len[0];
+  for (int li = 0; li < d->cfg.num_layers; ++li)
+    STRATA_REQUIRE(d->kv->len[li] == pos0,
+                   "cache_position must append exactly after the cached sequence; layer %d has "
+                   "length %d, layer 0 has %d",
+                   li, d->kv->len[li], pos0);
+  STRATA_REQUIRE(pos0 + L <= d->kv->Lmax, "KV cache capacity exceeded: %d + %d > Lmax %d", pos0,
+                 L, d->kv->Lmax);
+  return STRATA_OK;
+}
+
+void set_lengths(strata_decoder* d, int len) {
+  for (int& l : d->kv->len) l = len;
+}
+
+}  // namespace
+
+extern "C" {
+
+int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
+                          const uint16_t* embed, const uint16_t* final_norm,
+                          const uint16_t* lm_head, const strata_llama_layer* layers,
+                          strata_kv* kv, int max_batch, int max_tokens, strata_decoder** out) {
+  STRATA_REQUIRE(ctx && cfg && embed && final_norm && lm_head && layers && kv && out,
+                 "decoder_create: null argument");
+  const strata_llama_config& c = *cfg;
+  STRATA_REQUIRE(c.num_layers > 0 && c.hidden_size > 0 && c.num_heads > 0 && c.num_kv_heads > 0 &&
+                     c.head_dim > 0 && c.vocab_size > 0 && c.intermediate_size > 0,
+                 "decoder_create: invalid config");
+  STRATA_REQUIRE(c.num_heads % c.num_kv_heads == 0,
+                 "query heads must be divisible by key/value heads");
+  STRATA_REQUIRE(c.group_size == 64, "only group_size 64 is supported");
+  STRATA_REQUIRE(c.hidden_size % 64 == 0 && c.intermediate_size % 64 == 0 &&
+                     (c.num_heads * c.head_dim) % 64 == 0,
+                 "hidden, intermediate and head widths must be multiples of 64");
+  STRATA_REQUIRE(c.head_dim == 64 || c.head_dim == 128, "head_dim must be 64 or 128");
+  STRATA_REQUIRE(kv->layers == c.num_layers && kv->Hkv == c.num_kv_heads && kv->D == c.head_dim &&
+                     kv->dtype == STRATA_BF16,
+                 "KV cache geometry/dtype does not match the model (bf16 cache required)");
+  STRATA_REQUIRE(max_batch >= 1 && max_batch <= 8 && max_tokens >= max_batch,
+                 "max_batch must be in 1..8 and max_tokens >= max_batch");
+  auto* d = new strata_decoder{};
+  d->ctx = ctx;
+  d->cfg = c;
+  d->embed = embed;
+  d->final_norm = final_norm;
+  d->lm_head = lm_head;
+  d->layers.assign(layers, layers + c.num_layers);
+  d->kv = kv;
+  d->max_batch = max_batch;
+  d->max_tokens = max_tokens;
+  const size_t T = max_tokens;
+  const size_t H = c.hidden_size, F = c.intermediate_size, QW = (size_t)c.num_heads * c.head_dim,
+               KW = (size_t)c.num_kv_heads * c.head_dim;
+  int rc = STRATA_OK;
+  struct { void** p; size_t bytes; } bufs[] = {
+      {&d->h, T * H * 2},      {&d->xn, T * H * 2},     {&d->q, T * QW * 2},
+      {&d->k, T * KW * 2},     {&d->v, T * KW * 2},     {&d->qr, T * QW * 2},
+      {&d->attn, T * QW * 2},  {&d->o, T * H * 2},      {&d->gate, T * F * 2},
+      {&d->up, T * F * 2},     {&d->act, T * F * 2},    {&d->delta, T * H * 2},
+      {&d->hn, T * H * 2},
+      {reinterpret_cast<void**>(&d->logits), (size_t)max_batch * c.vocab_size * 4},
+      {reinterpret_cast<void**>(&d->ids), (size_t)max_batch * 4},
+      {reinterpret_cast<void**>(&d->counters), 16},
+      {&d->amax, (size_t)max_batch * kArgmaxBlocks * 8},
+  };
+  for (auto& b : bufs)
+    if (!rc) rc = alloc(b.p, b.bytes);
+  d->part_splits = strata_attn_decode_splits(ctx, kv->B, c.num_kv_heads, kv->Lmax);
+  if (!rc)
+    rc = alloc(reinterpret_cast<void**>(&d->part),
+               (size_t)kv->B * c.num_heads * d->part_splits * (c.head_dim + 2) * 4);
+  if (!rc) rc = alloc(reinterpret_cast<void**>(&d->tickets), (size_t)kv->B * c.num_kv_heads * 4);
+  if (!rc && hipMemset(d->tickets, 0, (size_t)kv->B * c.num_kv_heads * 4) != hipSuccess)
+    rc = strata_set_error(STRATA_EHIP, "decoder: ticket initialisation failed");
+  if (!rc && hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess)
+    rc = strata_set_error(STRATA_EHIP, "decoder: stream creation failed");
+  if (rc) {
+    strata_decoder_destroy(d);
+    return rc;
+  }
+  *out = d;
+  return STRATA_OK;
+}
+
+int strata_decoder_destroy(strata_decoder* d) {
+  if (!d) return STRATA_OK;
+  hipDeviceSynchronize();
+  if (d->graph) hipGraphExecDestroy(d->graph);
+  void* ptrs[] = {d->h, d->xn, d->q, d->k, d->v, d->qr, d->attn, d->o, d->gate, d->up, d->act,
+                  d->delta, d->hn, d->logits, d->ids, d->counters, d->part, d->tickets, d->amax};
+  for (void* p : ptrs)
+    if (p) hipFree(p);
+  if (d->stream) hipStreamDestroy(d->stream);
+  delete d;
+  return STRATA_OK;
+}
+
+int strata_decoder_forward(strata_decoder* d, const int32_t* ids, int B, int L, float* logits,
+                           void* stream) {
+  RC(check_forward(d, B, L));
+  STRATA_REQUIRE(ids != nullptr && logits != nullptr, "null ids/logits");
+  const int pos0 = d->kv->len[0];
+  const strata_llama_config& c = d->cfg;
+  RC(strata_embed_launch(d->embed, c.vocab_size, c.hidden_size, ids, (int64_t)B * L, d->h, stream));
+  RC(forward_layers(d, B, L, pos0, stream));
+  set_lengths(d, pos0 + L);
+  STRATA_HIP_CHECK(hipMemcpyAsync(logits, d->logits, (size_t)B * c.vocab_size * 4,
+                                  hipMemcpyDeviceToDevice, as_stream(stream)));
+  return STRATA_OK;
+}
+
+int strata_decoder_generate(strata_decoder* d, const int32_t* prompt, int B, int L, int max_new,
+                            float temperature, int use_graph, int32_t* out_tokens, void* stream) {
+  RC(check_forward(d, B, L));
+  STRATA_REQUIRE(prompt != nullptr && out_tokens != nullptr, "null prompt/out_tokens");
+  STRATA_REQUIRE(max_new >= 1, "max_new_tokens must be positive");
+  STRATA_REQUIRE(temperature > 0.f, "temperature must be positive");
+  const int pos0 = d->kv->len[0];
+  STRATA_REQUIRE(pos0 + L + max_new - 1 <= d->kv->Lmax,
+                 "KV cache capacity exceeded: %d + %d + %d - 1 > Lmax %d", pos0, L, max_new,
+                 d->kv->Lmax);
+  const strata_llama_config& c = d->cfg;
+  hipStream_t s = d->stream;
+  // order the decoder stream after the caller's work
+  hipEvent_t ev;
+  STRATA_HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  STRATA_HIP_CHECK(hipEventRecord(ev, as_stream(stream)));
+  STRATA_HIP_CHECK(hipStreamWaitEvent(s, ev, 0));
+  // prefill
+  RC(strata_embed_launch(d->embed, c.vocab_size, c.hidden_size, prompt, (int64_t)B * L, d->h, s));
+  RC(forward_layers(d, B, L, pos0, s));
+  RC(strata_argmax_launch(d->logits, B, c.vocab_size, temperature, d->ids, d->amax, s));
+  // counters {step, position, key count}: the advance below records token 0
+  // and leaves {1, pos0+L, pos0+L+1}, i.e. the next step processes the token
+  // at position pos0+L against pos0+L+1 keys.
+  const int init[4] = {0, pos0 + L - 1, pos0 + L, 0};
+  STRATA_HIP_CHECK(hipMemcpyAsync(d->counters, init, sizeof(init), hipMemcpyHostToDevice, s));
+  RC(strata_decode_advance_launch(d->ids, B, out_tokens, max_new, d->counters, s));
+
+  auto decode_step = [&](hipStream_t st) -> int {
+    RC(strata_embed_launch(d->embed, c.vocab_size, c.hidden_size, d->ids, B, d->h, st));
+    RC(forward_layers(d, B, 1, -1, st));
+    RC(strata_argmax_launch(d->logits, B, c.vocab_size, temperature, d->ids, d->amax, st));
+    RC(strata_decode_advance_launch(d->ids, B, out_tokens, max_new, d->counters, st));
+    return STRATA_OK;
+  };
+  if (max_new > 1) {
+    if (use_graph) {
+      const bool reuse = d->graph && d->graph_batch == B && d->graph_temp == temperature &&
+                         d->graph_out == out_tokens && d->graph_out_stride == max_new;
+      if (!reuse) {
+        if (d->graph) {
+          STRATA_HIP_CHECK(hipGraphExecDestroy(d->graph));
+          d->graph = nullptr;
+        }
+        hipGraph_t g;
+        STRATA_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        const int crc = decode_step(s);
+        const hipError_t ce = hipStreamEndCapture(s, &g);
+        if (crc) return crc;
+        if (ce != hipSuccess)
+          return strata_set_error(STRATA_EHIP, "decode graph capture failed: %s",
+                                  hipGetErrorString(ce));
+        const hipError_t ie = hipGraphInstantiate(&d->graph, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (ie != hipSuccess)
+          return strata_set_error(STRATA_EHIP, "decode graph instantiation failed: %s",
+                                  hipGetErrorString(ie));
+        d->graph_batch = B;
+        d->graph_temp = temperature;
+        d->graph_out = out_tokens;
+        d->graph_out_stride = max_new;
+      }
+      for (int i = 1; i < max_new; ++i) STRATA_HIP_CHECK(hipGraphLaunch(d->graph, s));
+    } else {
+      for (int i = 1; i < max_new; ++i) RC(decode_step(s));
+    }
+  }
+  STRATA_HIP_CHECK(hipEventRecord(ev, s));
+  STRATA_HIP_CHECK(hipStreamWaitEvent(as_stream(stream), ev, 0));
+  STRATA_HIP_CHECK(hipStreamSynchronize(s));
+  STRATA_HIP_CHECK(hipEventDestroy(ev));
+  set_lengths(d, pos0 + L + max_new - 1);
+  return STRATA_OK;
+}
+
+}  // extern "C"

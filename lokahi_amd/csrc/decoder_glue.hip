@@ -2,7 +2,7 @@
 // residual add, embedding gather, greedy argmax and the q4 weight quantizer.
 // These sit inside every decode step (src/ollm/llama_mlx.py:77-92, 399-407,
 // 647-653, 724-738; src/ollm/generation.py:42-43).
-#include "strata_common.h"
+#include "strata_internal.h"
 
 // Products and sums are rounded separately (no FMA contraction) so the glue
 // matches its CPU restatement operation by operation.
@@ -22,6 +22,72 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 }
 
 // One workgroup per row.  If res != nullptr: x <- bf16(x + res) first.
+// Vector path: each thread holds NV uint4 (8 bf16 each) of the row in
+// registers, so x is read once; the generic path re-reads x.
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ res,
+                                                          const uint16_t* __restrict__ w,
+                                                          int64_t H, float eps,
+                                                          uint16_t* __restrict__ y) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  uint4* xr = reinterpret_cast<uint4*>(x + row * H);
+  const uint4* rr = res ? reinterpret_cast<const uint4*>(res + row * H) : nullptr;
+  const uint4* wr = reinterpret_cast<const uint4*>(w);
+  uint4* yr = reinterpret_cast<uint4*>(y + row * H);
+  const int nvec = static_cast<int>(H >> 3);
+  float v[NV][8];
+  float ss = 0.f;
+  uint4 xa[NV], ra[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = min((int)threadIdx.x + 256 * j, nvec - 1);
+    xa[j] = xr[i];
+    ra[j] = rr ? rr[i] : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = threadIdx.x + 256 * j;
+    const uint32_t xu[4] = {xa[j].x, xa[j].y, xa[j].z, xa[j].w};
+    const uint32_t ru[4] = {ra[j].x, ra[j].y, ra[j].z, ra[j].w};
+    uint32_t hu[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float lo = __uint_as_float(xu[c] << 16), hi = __uint_as_float(xu[c] & 0xffff0000u);
+      if (rr) {
+        lo = bf16_to_f32(f32_to_bf16(lo + __uint_as_float(ru[c] << 16)));
+        hi = bf16_to_f32(f32_to_bf16(hi + __uint_as_float(ru[c] & 0xffff0000u)));
+      }
+      hu[c] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+      v[j][2 * c] = lo;
+      v[j][2 * c + 1] = hi;
+    }
+    if (i < nvec) {
+      if (rr) xr[i] = make_uint4(hu[0], hu[1], hu[2], hu[3]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[j][e], v[j][e], ss);
+    }
+  }
+  const float tot = block_sum256(ss, red);
+  const float r = 1.0f / sqrtf(tot / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = threadIdx.x + 256 * j;
+    if (i >= nvec) continue;
+    const uint4 wv = wr[i];
+    const uint32_t wu[4] = {wv.x, wv.y, wv.z, wv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float a = mul_rn(mul_rn(v[j][2 * c], r), __uint_as_float(wu[c] << 16));
+      const float bb = mul_rn(mul_rn(v[j][2 * c + 1], r), __uint_as_float(wu[c] & 0xffff0000u));
+      o[c] = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(bb)) << 16);
+    }
+    yr[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ res,
                                                       const uint16_t* __restrict__ w, int64_t H,
@@ -74,32 +140,62 @@ __global__ void embed_kernel(const uint16_t* __restrict__ table, int64_t V, int6
   for (int64_t i = threadIdx.x; i < H; i += blockDim.x) y[t * H + i] = table[id * H + i];
 }
 
-// One workgroup per row; ties resolve to the lowest index.
-__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, int64_t V,
-                                                     int32_t* __restrict__ out) {
-  __shared__ float sv[4];
-  __shared__ int si[4];
-  const float* lr = logits + blockIdx.x * V;
-  float best = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int64_t i = threadIdx.x; i < V; i += 256) {
-    const float v = lr[i];
-    if (v > best) { best = v; bi = static_cast<int>(i); }
-  }
+// Greedy argmax in two stages: grid (nb, rows) workgroups each reduce a
+// slice of the row to (value, index); one workgroup per row reduces the nb
+// partials.  Ties resolve to the lowest index.
+__device__ __forceinline__ void argmax_pick(float& best, int& bi, float v, int i) {
+  if (v > best || (v == best && i < bi)) { best = v; bi = i; }
+}
+
+__device__ __forceinline__ void argmax_block(float& best, int& bi, float* sv, int* si) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float ov = __shfl_xor(best, off, 64);
     const int oi = __shfl_xor(bi, off, 64);
-    if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+    argmax_pick(best, bi, ov, oi);
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) { sv[wave] = best; si[wave] = bi; }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; ++w)
-      if (sv[w] > best || (sv[w] == best && si[w] < bi)) { best = sv[w]; bi = si[w]; }
-    out[blockIdx.x] = bi == 0x7fffffff ? 0 : bi;
+  if (threadIdx.x == 0)
+    for (int w = 1; w < 4; ++w) argmax_pick(best, bi, sv[w], si[w]);
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ logits,
+                                                             int64_t V, float temperature,
+                                                             int slice, float* __restrict__ pv,
+                                                             int* __restrict__ pi) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int row = blockIdx.y;
+  const float* lr = logits + (int64_t)row * V;
+  const int64_t lo = (int64_t)blockIdx.x * slice;
+  const int64_t hi = min(V, lo + slice);
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+    // argmax(logits / T) as generation.py:42-43 evaluates it (fp32 divide)
+    const float v = temperature == 1.0f ? lr[i] : __fdiv_rn(lr[i], temperature);
+    argmax_pick(best, bi, v, static_cast<int>(i));
   }
+  argmax_block(best, bi, sv, si);
+  if (threadIdx.x == 0) {
+    pv[row * gridDim.x + blockIdx.x] = best;
+    pi[row * gridDim.x + blockIdx.x] = bi;
+  }
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restrict__ pv,
+                                                           const int* __restrict__ pi, int nb,
+                                                           int32_t* __restrict__ out) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int row = blockIdx.x;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < nb; i += 256) argmax_pick(best, bi, pv[row * nb + i], pi[row * nb + i]);
+  argmax_block(best, bi, sv, si);
+  if (threadIdx.x == 0) out[row] = bi == 0x7fffffff ? 0 : bi;
 }
 
 // One thread per group of 64.
@@ -146,6 +242,21 @@ inline int grid_for(int64_t n) {
 
 int strata_rmsnorm_launch(void* x, const void* res, const uint16_t* w, int64_t rows, int64_t H,
                           float eps, void* y, void* stream) {
+  const bool al = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(res) |
+                    reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(y)) & 15u) == 0;
+  if (al && H % 8 == 0 && H <= 8 * 256 * 4) {
+    const int nv = static_cast<int>((H / 8 + 255) / 256);
+    hipStream_t s = as_stream(stream);
+    uint16_t* xx = reinterpret_cast<uint16_t*>(x);
+    const uint16_t* rr = reinterpret_cast<const uint16_t*>(res);
+    uint16_t* yy = reinterpret_cast<uint16_t*>(y);
+    if (nv == 1) hipLaunchKernelGGL(rmsnorm_vec_kernel<1>, dim3(rows), dim3(256), 0, s, xx, rr, w, H, eps, yy);
+    else if (nv == 2) hipLaunchKernelGGL(rmsnorm_vec_kernel<2>, dim3(rows), dim3(256), 0, s, xx, rr, w, H, eps, yy);
+    else if (nv == 3) hipLaunchKernelGGL(rmsnorm_vec_kernel<3>, dim3(rows), dim3(256), 0, s, xx, rr, w, H, eps, yy);
+    else hipLaunchKernelGGL(rmsnorm_vec_kernel<4>, dim3(rows), dim3(256), 0, s, xx, rr, w, H, eps, yy);
+    STRATA_HIP_CHECK(hipGetLastError());
+    return STRATA_OK;
+  }
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, as_stream(stream),
                      reinterpret_cast<uint16_t*>(x), reinterpret_cast<const uint16_t*>(res), w, H,
                      eps, reinterpret_cast<uint16_t*>(y));
@@ -175,8 +286,17 @@ int strata_embed_launch(const uint16_t* table, int64_t V, int64_t H, const int32
   return STRATA_OK;
 }
 
-int strata_argmax_launch(const float* logits, int64_t rows, int64_t V, int32_t* out, void* stream) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, as_stream(stream), logits, V, out);
+int strata_argmax_launch(const float* logits, int64_t rows, int64_t V, float temperature,
+                         int32_t* out, void* partial, void* stream) {
+  // partial: rows * kArgmaxBlocks * 8 bytes (values then indices)
+  const int nb = kArgmaxBlocks;
+  const int slice = static_cast<int>((V + nb - 1) / nb);
+  float* pv = reinterpret_cast<float*>(partial);
+  int* pi = reinterpret_cast<int*>(pv + rows * nb);
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(nb, rows), dim3(256), 0, s, logits, V,
+                     temperature, slice, pv, pi);
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(256), 0, s, pv, pi, nb, out);
   STRATA_HIP_CHECK(hipGetLastError());
   return STRATA_OK;
 }
@@ -190,6 +310,31 @@ int strata_quantize_launch(const void* src, int dtype, int64_t N, int64_t K, int
   else
     hipLaunchKernelGGL((quantize_kernel<float>), dim3(grid_for(ng)), dim3(256), 0,
                        as_stream(stream), (const float*)src, N, K, G, w, s, b);
+  STRATA_HIP_CHECK(hipGetLastError());
+  return STRATA_OK;
+}
+
+namespace {
+// End of a graph-replayed decode step: record the token chosen for each batch
+// row, and advance the device counters {step, position, key count}.
+__global__ void decode_advance_kernel(const int32_t* __restrict__ ids, int B,
+                                      int32_t* __restrict__ out, int out_stride,
+                                      int* __restrict__ counters) {
+  const int step = counters[0];
+  for (int b = threadIdx.x; b < B; b += blockDim.x) out[(int64_t)b * out_stride + step] = ids[b];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    counters[0] = step + 1;
+    counters[1] += 1;
+    counters[2] += 1;
+  }
+}
+}  // namespace
+
+int strata_decode_advance_launch(const int32_t* ids, int B, int32_t* out_tokens, int out_stride,
+                                 int* counters, void* stream) {
+  hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(64), 0, as_stream(stream), ids, B,
+                     out_tokens, out_stride, counters);
   STRATA_HIP_CHECK(hipGetLastError());
   return STRATA_OK;
 }

@@ -77,8 +77,11 @@ __global__ void kv_copy(const TS* __restrict__ src, TC* __restrict__ dst, int B,
 template <typename TS, typename TC>
 __global__ void rope_kv_fused(const TS* __restrict__ qs, const TS* __restrict__ ks,
                               const TS* __restrict__ vs, int B, int Hq, int Hkv, int L, int D,
-                              int Lmax, int pos0, float theta, TS* __restrict__ q_out,
-                              TC* __restrict__ kc, TC* __restrict__ vc) {
+                              int Lmax, int pos0, const int* __restrict__ dpos, float theta,
+                              TS* __restrict__ q_out, TC* __restrict__ kc, TC* __restrict__ vc) {
+  // dpos (device) overrides pos0: the decode step replayed from a HIP graph
+  // reads its position from memory the previous step advanced.
+  if (dpos) pos0 = *dpos;
   const int half = D / 2;
   const int NH = Hq + 2 * Hkv;
   const int64_t total = (int64_t)B * L * NH * half;
@@ -175,18 +178,18 @@ int strata_kv_copy_launch(const void* src, int src_dtype, void* dst, int dst_dty
 
 int strata_rope_kv_fused_launch(const void* qs, const void* ks, const void* vs, int src_dtype,
                                 int B, int Hq, int Hkv, int L, int D, int Lmax, int pos0,
-                                float theta, void* q_out, void* kc, void* vc, int cache_dtype,
-                                void* stream) {
+                                const int* dpos, float theta, void* q_out, void* kc, void* vc,
+                                int cache_dtype, void* stream) {
   hipStream_t s = as_stream(stream);
   const int64_t n = (int64_t)B * L * (Hq + 2 * Hkv) * (D / 2);
   const dim3 g(grid_for(n)), blk(256);
   if (src_dtype == STRATA_BF16 && cache_dtype == STRATA_BF16)
     hipLaunchKernelGGL((rope_kv_fused<bf16_t, bf16_t>), g, blk, 0, s, (const bf16_t*)qs,
-                       (const bf16_t*)ks, (const bf16_t*)vs, B, Hq, Hkv, L, D, Lmax, pos0, theta,
+                       (const bf16_t*)ks, (const bf16_t*)vs, B, Hq, Hkv, L, D, Lmax, pos0, dpos, theta,
                        (bf16_t*)q_out, (bf16_t*)kc, (bf16_t*)vc);
   else if (src_dtype == STRATA_F32 && cache_dtype == STRATA_F32)
     hipLaunchKernelGGL((rope_kv_fused<float, float>), g, blk, 0, s, (const float*)qs,
-                       (const float*)ks, (const float*)vs, B, Hq, Hkv, L, D, Lmax, pos0, theta,
+                       (const float*)ks, (const float*)vs, B, Hq, Hkv, L, D, Lmax, pos0, dpos, theta,
                        (float*)q_out, (float*)kc, (float*)vc);
   else
     return strata_set_error(STRATA_ENOTSUP,

@@ -93,9 +93,22 @@ struct strata_ctx {
   int max_lds_per_block;
   void* scratch;        // device scratch arena (split-K partials), grown on demand
   size_t scratch_bytes;
+  int* tickets;         // zeroed split-K merge tickets (each launch leaves them zero)
+  int tickets_count;
 };
 
 // Returns a device scratch buffer of at least `bytes` (owned by ctx).
 int strata_ctx_scratch(strata_ctx* ctx, size_t bytes, void** out);
+// Returns at least `count` zeroed merge tickets (owned by ctx).
+int strata_ctx_tickets(strata_ctx* ctx, int count, int** out);
+
+// Optional inputs of the attention dispatcher used by the decoder engine.
+struct AttnExtra {
+  const int* dlen = nullptr;  // device key count (decode; overrides Lk, which is then capacity)
+  float* part = nullptr;      // caller-owned split-K partials [B, Hq, splits, D + 2]
+  int part_splits = 0;        // splits the partials buffer holds
+  int* tickets = nullptr;     // caller-owned zeroed merge tickets [B * Hkv]
+  int out_tm = 0;             // prefill: write token-major [B, Lq, Hq, D]
+};
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

@@ -1,0 +1,57 @@
+// Host-side declarations shared by the library's translation units: kernel
+// launchers (defined in the .hip files) and the KV-cache object.
+#pragma once
+
+#include <vector>
+
+#include "strata_common.h"
+
+inline bool dtype_ok(int d) { return d == STRATA_F32 || d == STRATA_BF16; }
+inline size_t dtype_size(int d) { return d == STRATA_F32 ? 4 : 2; }
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int strata_q4_gemv(strata_ctx* ctx, const void* x, int x_dtype, int M, int K,
+                   const strata_q4_weight* ws, int count, int y_dtype, void* stream);
+int strata_bf16_gemv(strata_ctx* ctx, const void* x, int M, int K, const uint16_t* w, int N,
+                     void* y, int y_dtype, void* stream);
+int strata_q4_gemm_launch(const void* x, int M, int K, const uint32_t* w, const uint16_t* s,
+                          const uint16_t* b, int N, void* y, int y_dtype, void* stream);
+int strata_attention_dispatch(strata_ctx* ctx, const void* q, int qd, const void* k, int kd,
+                              const void* v, int vd, int64_t kv_bs, int64_t kv_hs,
+                              const int32_t* qpos, int B, int Hq, int Hkv, int Lq, int Lk, int D,
+                              int causal, float eps, void* out, const AttnExtra& ex,
+                              void* stream);
+int strata_attn_decode_splits(strata_ctx* ctx, int B, int Hkv, int Lcap);
+int strata_rope_launch(void* q, void* k, const int32_t* pos, int B, int Hq, int Hkv, int L, int D,
+                       float theta, int dtype, void* stream);
+int strata_kv_copy_launch(const void* src, int src_dtype, void* dst, int dst_dtype, int B, int H,
+                          int Lnew, int Lmax, int D, int pos0, void* stream);
+int strata_rope_kv_fused_launch(const void* qs, const void* ks, const void* vs, int src_dtype,
+                                int B, int Hq, int Hkv, int L, int D, int Lmax, int pos0,
+                                const int* dpos, float theta, void* q_out, void* kc, void* vc,
+                                int cache_dtype, void* stream);
+int strata_rmsnorm_launch(void* x, const void* res, const uint16_t* w, int64_t rows, int64_t H,
+                          float eps, void* y, void* stream);
+int strata_silu_mul_launch(const void* g, const void* u, int64_t n, void* a, void* stream);
+int strata_add_launch(const void* x, const void* r, int64_t n, void* y, void* stream);
+int strata_embed_launch(const uint16_t* table, int64_t V, int64_t H, const int32_t* ids,
+                        int64_t n, void* y, void* stream);
+constexpr int kArgmaxBlocks = 128;  // workgroups per row of the first argmax stage
+int strata_argmax_launch(const float* logits, int64_t rows, int64_t V, float temperature,
+                         int32_t* out, void* partial, void* stream);
+int strata_quantize_launch(const void* src, int dtype, int64_t N, int64_t K, int G, uint32_t* w,
+                           uint16_t* s, uint16_t* b, void* stream);
+int strata_decode_advance_launch(const int32_t* ids, int B, int32_t* out_tokens, int out_stride,
+                                 int* counters, void* stream);
+
+struct strata_kv {
+  strata_ctx* ctx;
+  int layers, B, Hkv, Lmax, D, dtype;
+  void* k;
+  void* v;
+  bool owned;
+  std::vector<int> len;
+  size_t layer_elems() const { return (size_t)B * Hkv * Lmax * D; }
+  char* kl(int layer) const { return static_cast<char*>(k) + layer * layer_elems() * dtype_size(dtype); }
+  char* vl(int layer) const { return static_cast<char*>(v) + layer * layer_elems() * dtype_size(dtype); }
+};

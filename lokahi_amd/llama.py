@@ -154,9 +154,31 @@ class HipLlamaForCausalLM:
         return ops.linear(hn, self.w["lm_head"], None, None, out_dtype=torch.float32)
 
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 100,
-                 temperature: float = 1.0, past_key_values: Optional[HipKVCache] = None):
-        return greedy_generate(self, input_ids, max_new_tokens=max_new_tokens,
-                               temperature=temperature, past_key_values=past_key_values)
+                 temperature: float = 1.0, past_key_values: Optional[HipKVCache] = None,
+                 engine: bool = True, use_graph: bool = True):
+        """Greedy generation (``generation.py:7-50``).
+
+        ``engine=True`` runs the native decoder (prefill + HIP-graph decode
+        steps, tokens chosen on the device); ``engine=False`` drives the same
+        kernels op by op from Python.
+        """
+        if not engine:
+            return greedy_generate(self, input_ids, max_new_tokens=max_new_tokens,
+                                   temperature=temperature, past_key_values=past_key_values)
+        if max_new_tokens < 0:
+            raise ValueError("max_new_tokens must be non-negative")
+        if temperature <= 0:
+            raise ValueError("temperature must be positive")
+        if input_ids.ndim != 2 or input_ids.shape[1] == 0:
+            raise ValueError("input_ids must have shape [batch, sequence] with sequence > 0")
+        if max_new_tokens == 0:
+            return input_ids
+        B, L = input_ids.shape
+        cache = past_key_values
+        if cache is None:
+            cache = self.new_cache(B, L + max_new_tokens)
+        dec = DecoderEngine(self, cache, max_batch=B, max_tokens=B * L)
+        return dec.generate(input_ids, max_new_tokens, temperature, use_graph)
 
 
 @torch.no_grad()
@@ -185,3 +207,74 @@ def greedy_generate(model, input_ids: torch.Tensor, *, max_new_tokens: int,
         generated = torch.cat([generated.to(nxt.device), nxt], dim=1)
         model_input = nxt
     return generated
+
+
+class DecoderEngine:
+    """ctypes handle of the native ``strata_decoder`` for one model + KV cache."""
+
+    def __init__(self, model: "HipLlamaForCausalLM", cache: HipKVCache, max_batch: int = 1,
+                 max_tokens: int = 4096):
+        import ctypes as C
+        from . import _abi
+        from .ops import _ctx
+        cfg = model.config
+        w = model.w
+        self.model, self.cache = model, cache
+        self._lib = _abi.load()
+        dev = model.device.index or 0
+
+        def q4(name):
+            t = w[name + ".weight"]
+            return _abi.Q4Weight(t.data_ptr(), w[name + ".scales"].data_ptr(),
+                                 w[name + ".biases"].data_ptr(), t.shape[0], None)
+
+        layers = (_abi.LlamaLayerC * cfg.num_hidden_layers)()
+        for li in range(cfg.num_hidden_layers):
+            p = f"layers.{li}."
+            layers[li] = _abi.LlamaLayerC(
+                w[p + "input_layernorm"].data_ptr(), w[p + "post_attention_layernorm"].data_ptr(),
+                *[q4(p + n) for n in LINEARS])
+        ccfg = _abi.LlamaConfigC(cfg.vocab_size, cfg.hidden_size, cfg.intermediate_size,
+                                 cfg.num_hidden_layers, cfg.num_attention_heads,
+                                 cfg.num_key_value_heads, cfg.head_dim, cfg.group_size,
+                                 cfg.rms_norm_eps, cfg.rope_theta)
+        h = C.c_void_p()
+        _abi.check(self._lib.strata_decoder_create(
+            _ctx(dev), C.byref(ccfg), w["embed_tokens"].data_ptr(), w["norm"].data_ptr(),
+            w["lm_head"].data_ptr(), layers, cache.handle, max_batch, max_tokens, C.byref(h)))
+        self.handle = h
+        self._layers = layers  # keep the struct array alive with the handle
+        self.vocab = cfg.vocab_size
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        """Last-position fp32 logits [B, vocab] for ids [B, L] appended to the cache."""
+        import ctypes as C
+        from . import _abi
+        from .ops import _stream
+        ids32 = ids.to(device=self.model.device, dtype=torch.int32).contiguous()
+        B, L = ids32.shape
+        out = torch.empty((B, self.vocab), dtype=torch.float32, device=self.model.device)
+        _abi.check(self._lib.strata_decoder_forward(self.handle, ids32.data_ptr(), B, L,
+                                                    out.data_ptr(),
+                                                    _stream(self.model.device.index or 0)))
+        return out
+
+    def generate(self, prompt: torch.Tensor, max_new: int, temperature: float = 1.0,
+                 use_graph: bool = True) -> torch.Tensor:
+        from . import _abi
+        from .ops import _stream
+        ids32 = prompt.to(device=self.model.device, dtype=torch.int32).contiguous()
+        B, L = ids32.shape
+        out = torch.empty((B, max_new), dtype=torch.int32, device=self.model.device)
+        _abi.check(self._lib.strata_decoder_generate(
+            self.handle, ids32.data_ptr(), B, L, max_new, float(temperature),
+            1 if use_graph else 0, out.data_ptr(), _stream(self.model.device.index or 0)))
+        return torch.cat([prompt.to(out.device, torch.int64), out.to(torch.int64)], dim=1)
+
+    def __del__(self):
+        try:
+            if getattr(self, "handle", None):
+                self._lib.strata_decoder_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
