@@ -48,26 +48,6 @@ int strata_ctx_scratch(strata_ctx* ctx, size_t bytes, void** out) {
   return STRATA_OK;
 }
 
-int strata_ctx_tickets(strata_ctx* ctx, int count, int** out) {
-  if (count > ctx->tickets_count) {
-    if (ctx->tickets) {
-      STRATA_HIP_CHECK(hipDeviceSynchronize());
-      STRATA_HIP_CHECK(hipFree(ctx->tickets));
-      ctx->tickets = nullptr;
-      ctx->tickets_count = 0;
-    }
-    const int n = count < 4096 ? 4096 : count;
-    if (hipMalloc(&ctx->tickets, (size_t)n * sizeof(int)) != hipSuccess) {
-      ctx->tickets = nullptr;
-      return strata_set_error(STRATA_ENOMEM, "ticket allocation failed");
-    }
-    STRATA_HIP_CHECK(hipMemset(ctx->tickets, 0, (size_t)n * sizeof(int)));
-    ctx->tickets_count = n;
-  }
-  *out = ctx->tickets;
-  return STRATA_OK;
-}
-
 extern "C" {
 
 int strata_abi_version(void) { return STRATA_ABI_VERSION; }
@@ -99,7 +79,6 @@ int strata_ctx_destroy(strata_ctx* ctx) {
   if (!ctx) return STRATA_OK;
   hipDeviceSynchronize();
   if (ctx->scratch) hipFree(ctx->scratch);
-  if (ctx->tickets) hipFree(ctx->tickets);
   delete ctx;
   return STRATA_OK;
 }

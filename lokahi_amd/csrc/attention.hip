@@ -11,7 +11,7 @@
 //     streams one key chunk of one KV head for all G = Hq/Hkv query heads
 //     (K/V read once per group), keeps per-16-lane online-softmax state in
 //     registers, merges its lanes through LDS and writes (m, s, o[D]) partials;
-//     the last workgroup of each KV head merges all chunks in the same launch.
+//     attn_decode_merge combines the chunks.
 //   * attn_prefill_mfma : Lq > 1, D in {64, 128}, q/k/v of one dtype.
 //     Flash-style: 64-key K / V^T tiles staged in LDS, S^T = K Q^T and
 //     O^T += V^T P^T on MFMA (bf16 16x16x32, or f32 16x16x4 for fp32 inputs),
@@ -61,9 +61,9 @@ __device__ __forceinline__ void load_elems(const T* p, float* out) {
 // --------------------------------------------------------------- decode (Lq=1)
 // grid (nsplit, Hkv, B), block 256.  Each workgroup reduces one key chunk of
 // one KV head for its G query heads to (m, s, o[D]) per head.  With several
-// chunks the partials go to part [B, Hq, nsplit, D + 2] = (o[0..D), m, s);
-// the last workgroup of a (b, hkv) group to arrive (agent-scope ticket) merges
-// them and writes the output, then resets its ticket for the next launch.
+// chunks the partials go to part [B, Hq, nsplit, D + 2] = (o[0..D), m, s) and
+// attn_decode_merge combines them (the kernel boundary orders the partials'
+// writes before the merge's reads on every XCD).
 constexpr int kMaxDecodeSplits = 256;
 
 template <typename TQ, typename TK, typename TV, int D, int G>
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const TQ* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
     int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Hkv, int Lk,
     const int* __restrict__ dlen, int causal, int chunk, int nsplit, float scale, float eps,
-    float* __restrict__ part, int* __restrict__ tickets, TQ* __restrict__ out) {
+    float* __restrict__ part, TQ* __restrict__ out) {
   constexpr int EPL = 16 / sizeof(TK);          // key elements per lane
   constexpr int LPK = D / EPL;                  // lanes per key
   constexpr int KPW = 64 / LPK;                 // keys per wave step
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         float d = 0.f;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) d = fmaf(qv[g][e], kx[jj][e], d);
-        d = group_sum(d, LPK);
+        d = group_sum<LPK>(d);
         sc[jj] = (base + jj * 4 * KPW + sub < t1) ? d * sl2 : -INFINITY;  // log2 domain
         mb = fmaxf(mb, sc[jj]);
       }
@@ -159,9 +159,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   // ---- merge the KPW streams of each wave with shuffles, then the 4 waves in LDS
   __shared__ float sm_m[4][G], sm_s[4][G];
   __shared__ float sm_o[4][G][D];
-  __shared__ float sm_w[G][kMaxDecodeSplits];
-  __shared__ float sm_S[G];
-  __shared__ int sm_last;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     float mw = m[g];
@@ -202,49 +199,51 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       if (d == 0) { pp[D] = mx; pp[D + 1] = ss; }
     }
   }
-  if (nsplit == 1) return;
+}
 
-  // ---- cross-chunk merge by the last workgroup of this (b, hkv)
-  __threadfence();  // every thread publishes its partial stores device-wide
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int* t = tickets + b * Hkv + hkv;
-    const int prev = __hip_atomic_fetch_add(t, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = prev == nsplit - 1;
-    if (last) __hip_atomic_store(t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sm_last = last;
+// grid (B*Hq), block 256: combine the nsplit partials of one (b, hq).  All
+// (m, s) pairs are loaded in parallel, the weights exp2(m_i - max) computed
+// once in LDS, then each thread sums its head-dim entries over the chunks.
+template <typename TQ>
+__global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict__ part,
+                                                         int nsplit, int D, float eps,
+                                                         TQ* __restrict__ out) {
+  __shared__ float sw[kMaxDecodeSplits];
+  __shared__ float red[4];
+  __shared__ float s_tot;
+  const int bh = blockIdx.x;
+  const float* pp = part + (int64_t)bh * nsplit * (D + 2);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < nsplit; i += 256) {
+    const float si = pp[(int64_t)i * (D + 2) + D + 1];
+    const float mi = si > 0.f ? pp[(int64_t)i * (D + 2) + D] : -INFINITY;
+    sw[i] = mi;
+    mx = fmaxf(mx, mi);
   }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) red[wave] = mx;
   __syncthreads();
-  if (!sm_last) return;
-  __atomic_thread_fence(__ATOMIC_ACQUIRE);  // see every chunk's partials
-  const float* pb = part + ((int64_t)b * Hq + hkv * G) * nsplit * (D + 2);
-  for (int idx = threadIdx.x; idx < G * nsplit; idx += 256) {
-    const int g = idx / nsplit, i = idx - g * nsplit;
-    const float* pp = pb + ((int64_t)g * nsplit + i) * (D + 2);
-    sm_w[g][i] = pp[D + 1] > 0.f ? pp[D] : -INFINITY;   // chunk max (log2 domain)
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < nsplit; i += 256) {
+    const float w = sw[i] == -INFINITY ? 0.f : exp2f(sw[i] - mx);
+    sw[i] = w;
+    ss = fmaf(pp[(int64_t)i * (D + 2) + D + 1], w, ss);
   }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
   __syncthreads();
-  if (threadIdx.x < G) {
-    const int g = threadIdx.x;
-    float mx = -INFINITY;
-    for (int i = 0; i < nsplit; ++i) mx = fmaxf(mx, sm_w[g][i]);
-    float ss = 0.f;
-    for (int i = 0; i < nsplit; ++i) {
-      const float* pp = pb + ((int64_t)g * nsplit + i) * (D + 2);
-      const float wgt = sm_w[g][i] == -INFINITY ? 0.f : exp2f(sm_w[g][i] - mx);
-      sm_w[g][i] = wgt;
-      ss = fmaf(pp[D + 1], wgt, ss);
-    }
-    sm_S[g] = ss;
-  }
+  if (threadIdx.x == 0) s_tot = (red[0] + red[1]) + (red[2] + red[3]);
   __syncthreads();
-  for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-    const int g = idx / D, d = idx - g * D;
-    const float* pp = pb + (int64_t)g * nsplit * (D + 2) + d;
+  const float inv = 1.f / fmaxf(s_tot, eps);
+  for (int d = threadIdx.x; d < D; d += 256) {
     float oo = 0.f;
 #pragma unroll 8
-    for (int i = 0; i < nsplit; ++i) oo = fmaf(pp[(int64_t)i * (D + 2)], sm_w[g][i], oo);
-    Elem<TQ>::store(out, ((int64_t)b * Hq + hkv * G + g) * D + d, oo / fmaxf(sm_S[g], eps));
+    for (int i = 0; i < nsplit; ++i) oo = fmaf(pp[(int64_t)i * (D + 2) + d], sw[i], oo);
+    Elem<TQ>::store(out, (int64_t)bh * D + d, oo * inv);
   }
 }
 
@@ -524,20 +523,16 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
   int nsplit, chunk;
   decode_split_geometry(ctx->num_cus, B, Hkv, Lk, &nsplit, &chunk);
   float* part = nullptr;
-  int* tickets = nullptr;
   if (nsplit > 1) {
-    if (ex.part) {  // decoder-owned partials and tickets (graph-safe)
-      if (ex.part_splits < nsplit || !ex.tickets)
+    if (ex.part) {  // decoder-owned partials (graph-safe: no allocation)
+      if (ex.part_splits < nsplit)
         return strata_set_error(STRATA_EINVAL, "decode attention: partials buffer too small");
       part = ex.part;
-      tickets = ex.tickets;
     } else {
       void* p = nullptr;
       const int rc = strata_ctx_scratch(ctx, (size_t)B * Hq * nsplit * (D + 2) * sizeof(float), &p);
       if (rc) return rc;
       part = reinterpret_cast<float*>(p);
-      const int rt = strata_ctx_tickets(ctx, B * Hkv, &tickets);
-      if (rt) return rt;
     }
   }
   dim3 grid(nsplit, Hkv, B);
@@ -545,12 +540,16 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
   if (G == GV)                                                                                \
     hipLaunchKernelGGL((attn_decode_kernel<TQ, TK, TV, D, GV>), grid, dim3(256), 0, stream,   \
                        (const TQ*)q, (const TK*)k, (const TV*)v, kv_bs, kv_hs, qpos, Hq, Hkv, \
-                       Lk, ex.dlen, causal, chunk, nsplit, scale, eps, part, tickets,         \
-                       (TQ*)out);
+                       Lk, ex.dlen, causal, chunk, nsplit, scale, eps, part, (TQ*)out);
   STRATA_DEC(1) else STRATA_DEC(2) else STRATA_DEC(4) else STRATA_DEC(8) else
     return strata_set_error(STRATA_ENOTSUP, "decode attention: group size %d not in {1,2,4,8}", G);
 #undef STRATA_DEC
   STRATA_HIP_CHECK(hipGetLastError());
+  if (nsplit > 1) {
+    hipLaunchKernelGGL((attn_decode_merge<TQ>), dim3(B * Hq), dim3(256), 0, stream, part, nsplit,
+                       D, eps, (TQ*)out);
+    STRATA_HIP_CHECK(hipGetLastError());
+  }
   return STRATA_OK;
 }
 

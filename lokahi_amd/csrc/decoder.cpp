@@ -39,7 +39,6 @@ struct strata_decoder {
   int* counters;          // {step, position, key count}
   float* part;            // split-K partials for graph-mode decode attention
   int part_splits;
-  int* tickets;           // split-K merge tickets [B * Hkv], zeroed once
   void* amax;             // argmax partials [max_batch * kArgmaxBlocks * 8 B]
   hipStream_t stream;     // the decoder's own stream (graph capture / replay)
   hipGraphExec_t graph;   // captured decode step
@@ -100,7 +99,6 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream) {
       ex.dlen = d->counters + 2;
       ex.part = d->part;
       ex.part_splits = d->part_splits;
-      ex.tickets = d->tickets;
       RC(strata_attention_dispatch(d->ctx, d->qr, STRATA_BF16, kc, STRATA_BF16, vc, STRATA_BF16,
                                    kv_bs, kv_hs, nullptr, B, Hq, Hkv, 1, kv->Lmax, D, 1, 1e-12f,
                                    d->attn, ex, stream));
@@ -226,9 +224,6 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
   if (!rc)
     rc = alloc(reinterpret_cast<void**>(&d->part),
                (size_t)kv->B * c.num_heads * d->part_splits * (c.head_dim + 2) * 4);
-  if (!rc) rc = alloc(reinterpret_cast<void**>(&d->tickets), (size_t)kv->B * c.num_kv_heads * 4);
-  if (!rc && hipMemset(d->tickets, 0, (size_t)kv->B * c.num_kv_heads * 4) != hipSuccess)
-    rc = strata_set_error(STRATA_EHIP, "decoder: ticket initialisation failed");
   if (!rc && hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess)
     rc = strata_set_error(STRATA_EHIP, "decoder: stream creation failed");
   if (rc) {
@@ -244,7 +239,7 @@ int strata_decoder_destroy(strata_decoder* d) {
   hipDeviceSynchronize();
   if (d->graph) hipGraphExecDestroy(d->graph);
   void* ptrs[] = {d->h, d->xn, d->q, d->k, d->v, d->qr, d->attn, d->o, d->gate, d->up, d->act,
-                  d->delta, d->hn, d->logits, d->ids, d->counters, d->part, d->tickets, d->amax};
+                  d->delta, d->hn, d->logits, d->ids, d->counters, d->part, d->amax};
   for (void* p : ptrs)
     if (p) hipFree(p);
   if (d->stream) hipStreamDestroy(d->stream);

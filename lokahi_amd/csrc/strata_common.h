@@ -58,16 +58,31 @@ template <> struct Elem<bf16_t> {
 };
 
 // ---------------------------------------------------------------- wave helpers
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+// Cross-lane sums on DPP (no LDS round trip): within quads by quad_perm, then
+// 8- and 16-lane rows by row_half_mirror / row_mirror; wider groups finish
+// with xor shuffles.  After dpp_sum<W> every lane holds the sum of its
+// aligned group of W lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+template <int W>
+__device__ __forceinline__ float dpp_sum(float v) {
+  static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "width");
+  if constexpr (W >= 2) v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
+  if constexpr (W >= 4) v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+  if constexpr (W >= 8) v += dpp_f<0x141>(v);   // row_half_mirror
+  if constexpr (W >= 16) v += dpp_f<0x140>(v);  // row_mirror
+  if constexpr (W >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (W >= 64) v += __shfl_xor(v, 32, 64);
   return v;
 }
 
-__device__ __forceinline__ float group_sum(float v, int width) {
-  for (int off = width >> 1; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return dpp_sum<64>(v); }
+
+template <int W>
+__device__ __forceinline__ float group_sum(float v) { return dpp_sum<W>(v); }
 
 // ---------------------------------------------------------------- host helpers
 // Thread-local error message; every entry point returns a status code and
@@ -93,21 +108,16 @@ struct strata_ctx {
   int max_lds_per_block;
   void* scratch;        // device scratch arena (split-K partials), grown on demand
   size_t scratch_bytes;
-  int* tickets;         // zeroed split-K merge tickets (each launch leaves them zero)
-  int tickets_count;
 };
 
 // Returns a device scratch buffer of at least `bytes` (owned by ctx).
 int strata_ctx_scratch(strata_ctx* ctx, size_t bytes, void** out);
-// Returns at least `count` zeroed merge tickets (owned by ctx).
-int strata_ctx_tickets(strata_ctx* ctx, int count, int** out);
 
 // Optional inputs of the attention dispatcher used by the decoder engine.
 struct AttnExtra {
   const int* dlen = nullptr;  // device key count (decode; overrides Lk, which is then capacity)
   float* part = nullptr;      // caller-owned split-K partials [B, Hq, splits, D + 2]
   int part_splits = 0;        // splits the partials buffer holds
-  int* tickets = nullptr;     // caller-owned zeroed merge tickets [B * Hkv]
   int out_tm = 0;             // prefill: write token-major [B, Lq, Hq, D]
 };
 
