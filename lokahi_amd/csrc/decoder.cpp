@@ -74,6 +74,8 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream) {
   strata_kv* kv = d->kv;
   const int64_t kv_bs = (int64_t)Hkv * kv->Lmax * D, kv_hs = (int64_t)kv->Lmax * D;
   const bool graph_mode = pos0 < 0;
+  // One-token steps (T <= 8 rows) fuse RoPE/append and SiLU into GEMV epilogues.
+  const bool decode = L == 1 && T <= 8;
   for (int li = 0; li < c.num_layers; ++li) {
     const strata_llama_layer& Lw = d->layers[li];
     RC(strata_rmsnorm_launch(d->h, li == 0 ? nullptr : d->delta, Lw.input_norm, T, H,
@@ -82,18 +84,22 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream) {
     qkv[0].y = d->q;
     qkv[1].y = d->k;
     qkv[2].y = d->v;
-    if (T <= 8) {
-      RC(strata_q4_gemv(d->ctx, d->xn, STRATA_BF16, T, H, qkv, 3, STRATA_BF16, stream));
+    void* kc = kv->kl(li);
+    void* vc = kv->vl(li);
+    if (decode) {
+      // q/k/v GEMV whose epilogue applies RoPE and appends k, v to the cache
+      GemvEpilogue e{2, D, Hq, Hkv, kv->Lmax, graph_mode ? 0 : pos0,
+                     graph_mode ? d->counters + 1 : nullptr, c.rope_theta,
+                     (uint16_t*)d->qr, (uint16_t*)kc, (uint16_t*)vc};
+      RC(strata_q4_gemv_epi(d->ctx, d->xn, T, H, qkv, 3, e, stream));
     } else {
       for (auto& w : qkv)
         RC(strata_q4_gemm_launch(d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
                                  stream));
+      RC(strata_rope_kv_fused_launch(d->q, d->k, d->v, STRATA_BF16, B, Hq, Hkv, L, D, kv->Lmax,
+                                     pos0, nullptr, c.rope_theta, d->qr, kc, vc, STRATA_BF16,
+                                     stream));
     }
-    void* kc = kv->kl(li);
-    void* vc = kv->vl(li);
-    RC(strata_rope_kv_fused_launch(d->q, d->k, d->v, STRATA_BF16, B, Hq, Hkv, L, D, kv->Lmax,
-                                   graph_mode ? 0 : pos0, graph_mode ? d->counters + 1 : nullptr,
-                                   c.rope_theta, d->qr, kc, vc, STRATA_BF16, stream));
     AttnExtra ex;
     if (graph_mode) {
       ex.dlen = d->counters + 2;
@@ -110,24 +116,27 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream) {
     }
     strata_q4_weight o = Lw.o;
     o.y = d->o;
-    if (T <= 8) RC(strata_q4_gemv(d->ctx, d->attn, STRATA_BF16, T, Hq * D, &o, 1, STRATA_BF16, stream));
+    if (decode) RC(strata_q4_gemv(d->ctx, d->attn, STRATA_BF16, T, Hq * D, &o, 1, STRATA_BF16, stream));
     else RC(strata_q4_gemm_launch(d->attn, T, Hq * D, o.w, o.scales, o.biases, (int)o.N, o.y,
                                   STRATA_BF16, stream));
     RC(strata_rmsnorm_launch(d->h, d->o, Lw.post_norm, T, H, c.rms_norm_eps, d->xn, stream));
     strata_q4_weight gu[2] = {Lw.gate, Lw.up};
     gu[0].y = d->gate;
     gu[1].y = d->up;
-    if (T <= 8) {
-      RC(strata_q4_gemv(d->ctx, d->xn, STRATA_BF16, T, H, gu, 2, STRATA_BF16, stream));
+    if (decode) {
+      // gate/up GEMV whose epilogue writes silu(gate) * up
+      gu[0].y = d->act;
+      GemvEpilogue e{1, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr};
+      RC(strata_q4_gemv_epi(d->ctx, d->xn, T, H, gu, 2, e, stream));
     } else {
       for (auto& w : gu)
         RC(strata_q4_gemm_launch(d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
                                  stream));
+      RC(strata_silu_mul_launch(d->gate, d->up, (int64_t)T * F, d->act, stream));
     }
-    RC(strata_silu_mul_launch(d->gate, d->up, (int64_t)T * F, d->act, stream));
     strata_q4_weight dn = Lw.down;
     dn.y = d->delta;
-    if (T <= 8) RC(strata_q4_gemv(d->ctx, d->act, STRATA_BF16, T, F, &dn, 1, STRATA_BF16, stream));
+    if (decode) RC(strata_q4_gemv(d->ctx, d->act, STRATA_BF16, T, F, &dn, 1, STRATA_BF16, stream));
     else RC(strata_q4_gemm_launch(d->act, T, F, dn.w, dn.scales, dn.biases, (int)dn.N, dn.y,
                                   STRATA_BF16, stream));
   }

@@ -21,7 +21,7 @@
 //   * lanes reduce with xor-butterflies at the end; results are deterministic.
 #include <cstdlib>
 
-#include "strata_common.h"
+#include "strata_internal.h"
 
 namespace {
 
@@ -37,10 +37,33 @@ struct Q4Problem {
   int row0;
 };
 
+// Epilogues (decode engine), chosen by Q4Batch::epi:
+//   EPI_STORE     : y[m, n] = bf16/fp32(acc)
+//   EPI_SILU_PAIR : problems 0/1 = gate/up with rows interleaved (row 2n is
+//                   gate n, row 2n+1 is up n, both in one wave); writes
+//                   y0[m, n] = bf16(silu(bf16(gate)) * bf16(up))
+//                   (llama_mlx.py:399-407) - the gate/up outputs never
+//                   leave registers;
+//   EPI_ROPE_KV   : problems 0/1/2 = q/k/v; inside each head the rows are
+//                   ordered (0, D/2, 1, D/2+1, ...) so a wave holds a RoPE
+//                   pair; writes rotated q head-major to q_out, rotated k and
+//                   v into the KV cache at the step's position
+//                   (llama_mlx.py:271-297; values are rounded to bf16 before
+//                   RoPE, as the separate kernels do).
+enum { EPI_STORE = 0, EPI_SILU_PAIR = 1, EPI_ROPE_KV = 2 };
+
 struct Q4Batch {
   Q4Problem p[kMaxProblems];
   int count;
   int total_rows;
+  int epi;
+  // EPI_ROPE_KV
+  int head_dim, n_heads, n_kv_heads, lmax, pos0;
+  const int* dpos;  // device position (graph-replayed step) or nullptr
+  float theta;
+  uint16_t* q_out;  // [M, Hq, 1, D] bf16
+  uint16_t* kc;     // cache layer [M, Hkv, lmax, D] bf16
+  uint16_t* vc;
 };
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
@@ -194,11 +217,20 @@ __global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__
   for (int r = 0; r < R; ++r) {
     const int row = (blockIdx.x * NW + wave) * R + r;
     valid[r] = row < batch.total_rows;
-    int pi = 0;
+    int pi = 0, n = 0;
+    if (batch.epi == EPI_SILU_PAIR) {
+      pi = row & 1;
+      n = valid[r] ? row >> 1 : 0;
+    } else {
 #pragma unroll
-    for (int t = 1; t < kMaxProblems; ++t)
-      if (t < batch.count && row >= batch.p[t].row0) pi = t;
-    const int n = valid[r] ? row - batch.p[pi].row0 : 0;
+      for (int t = 1; t < kMaxProblems; ++t)
+        if (t < batch.count && row >= batch.p[t].row0) pi = t;
+      n = valid[r] ? row - batch.p[pi].row0 : 0;
+      if (batch.epi == EPI_ROPE_KV) {  // (h, 2p + w) -> h*D + p + w*D/2
+        const int D = batch.head_dim, j = n % D;
+        n = n - j + (j >> 1) + (j & 1) * (D >> 1);
+      }
+    }
     pid[r] = pi;
     nloc[r] = n;
     wp[r] = batch.p[pi].w + (int64_t)n * nv;
@@ -312,6 +344,45 @@ __global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int mm = 0; mm < MT; ++mm) acc[r][mm] = wave_sum(acc[r][mm]);
+  if constexpr (R == 2) {
+    if (batch.epi != EPI_STORE) {
+#pragma unroll
+      for (int mm = 0; mm < MT; ++mm) {
+        const int m = m0 + mm;
+        if (lane != mm || !valid[0] || m >= M) continue;
+        const float a0 = bf16_to_f32(f32_to_bf16(acc[0][mm]));
+        const float a1 = bf16_to_f32(f32_to_bf16(acc[1][mm]));
+        if (batch.epi == EPI_SILU_PAIR) {
+          const float sg = a0 / (1.0f + expf(-a0));
+          const Q4Problem& p = batch.p[0];
+          store_y<bf16_t>(p.y, (int64_t)m * p.n + nloc[0], mul_rn(sg, a1));
+        } else {
+          const int D = batch.head_dim, half = D >> 1;
+          const int h = nloc[0] / D, i = nloc[0] - h * D;  // i < D/2: pair (i, i + D/2)
+          const int pos = batch.dpos ? *batch.dpos : batch.pos0;
+          if (pid[0] == 2) {  // v: copy into the cache
+            const int64_t co = (((int64_t)m * batch.n_kv_heads + h) * batch.lmax + pos) * D;
+            batch.vc[co + i] = f32_to_bf16(a0);
+            batch.vc[co + i + half] = f32_to_bf16(a1);
+          } else {
+            float c, sn, o1, o2;
+            rope_cs(pos, i, D, batch.theta, &c, &sn);
+            rotate_pair(a0, a1, c, sn, &o1, &o2);
+            if (pid[0] == 0) {
+              const int64_t qo = ((int64_t)m * batch.n_heads + h) * D;
+              batch.q_out[qo + i] = f32_to_bf16(o1);
+              batch.q_out[qo + i + half] = f32_to_bf16(o2);
+            } else {
+              const int64_t co = (((int64_t)m * batch.n_kv_heads + h) * batch.lmax + pos) * D;
+              batch.kc[co + i] = f32_to_bf16(o1);
+              batch.kc[co + i + half] = f32_to_bf16(o2);
+            }
+          }
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -494,6 +565,60 @@ int dispatch_q4(strata_ctx* ctx, const void* x, int M, int K, const Q4Batch& bat
 }
 
 }  // namespace
+
+int strata_q4_gemv_epi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
+                       int count, const GemvEpilogue& e, void* stream) {
+  STRATA_REQUIRE(e.mode == EPI_SILU_PAIR || e.mode == EPI_ROPE_KV, "unknown GEMV epilogue");
+  Q4Batch batch{};
+  batch.count = count;
+  batch.epi = e.mode;
+  int rows = 0;
+  for (int i = 0; i < count; ++i) {
+    batch.p[i].w = reinterpret_cast<const uint4*>(ws[i].w);
+    batch.p[i].s = ws[i].scales;
+    batch.p[i].b = ws[i].biases;
+    batch.p[i].y = ws[i].y;
+    batch.p[i].n = static_cast<int>(ws[i].N);
+    batch.p[i].row0 = rows;
+    rows += static_cast<int>(ws[i].N);
+  }
+  batch.total_rows = rows;
+  if (e.mode == EPI_SILU_PAIR)
+    STRATA_REQUIRE(count == 2 && ws[0].N == ws[1].N, "SiLU pair epilogue needs gate/up of one size");
+  if (e.mode == EPI_ROPE_KV) {
+    STRATA_REQUIRE(count == 3 && e.head_dim % 2 == 0 &&
+                       ws[0].N == (int64_t)e.n_heads * e.head_dim &&
+                       ws[1].N == (int64_t)e.n_kv_heads * e.head_dim && ws[2].N == ws[1].N,
+                   "RoPE/KV epilogue needs q/k/v of [Hq*D, Hkv*D, Hkv*D] rows");
+    batch.head_dim = e.head_dim;
+    batch.n_heads = e.n_heads;
+    batch.n_kv_heads = e.n_kv_heads;
+    batch.lmax = e.lmax;
+    batch.pos0 = e.pos0;
+    batch.dpos = e.dpos;
+    batch.theta = e.theta;
+    batch.q_out = e.q_out;
+    batch.kc = e.kc;
+    batch.vc = e.vc;
+  }
+  // both epilogues need a wave to own a row pair: R = 2 with even row blocks
+  const int nv = K / 32;
+  const int MT = M >= 4 ? 4 : (M >= 2 ? 2 : 1);
+  STRATA_REQUIRE(M <= 8 && (size_t)MT * nv * 68 <= (size_t)ctx->max_lds_per_block &&
+                     MT * nv <= 2 * 4 * 64 && nv <= 64 * 8,
+                 "GEMV epilogue: unsupported shape M=%d K=%d", M, K);
+  const int u = nv <= 128 ? 2 : (nv <= 256 ? 4 : (nv <= 448 ? 7 : 8));
+  const size_t lds = (size_t)MT * nv * 68;
+  GemvShape g{4, 2, u, MT};
+  hipStream_t s = as_stream(stream);
+  bool ok;
+  if (MT == 4) ok = launch_q4_u<4, 2, 4, bf16_t, bf16_t>(g, x, M, K, batch, lds, s);
+  else if (MT == 2) ok = launch_q4_u<4, 2, 2, bf16_t, bf16_t>(g, x, M, K, batch, lds, s);
+  else ok = launch_q4_u<4, 2, 1, bf16_t, bf16_t>(g, x, M, K, batch, lds, s);
+  if (!ok) return strata_set_error(STRATA_EINVAL, "GEMV epilogue: no kernel for K=%d", K);
+  STRATA_HIP_CHECK(hipGetLastError());
+  return STRATA_OK;
+}
 
 int strata_q4_gemv(strata_ctx* ctx, const void* x, int x_dtype, int M, int K,
                    const strata_q4_weight* ws, int count, int y_dtype, void* stream) {

@@ -16,24 +16,6 @@
 
 namespace {
 
-__device__ __forceinline__ void rope_cs(int pos, int i, int D, float theta, float* c, float* s) {
-#pragma clang fp contract(off)
-  const float inv = static_cast<float>(1.0 / pow(static_cast<double>(theta),
-                                                 static_cast<double>(2 * i) / D));
-  const float ang = mul_rn(static_cast<float>(pos), inv);
-  double sd, cd;
-  sincos(static_cast<double>(ang), &sd, &cd);
-  *c = static_cast<float>(cd);
-  *s = static_cast<float>(sd);
-}
-
-__device__ __forceinline__ void rotate_pair(float x1, float x2, float c, float s, float* o1,
-                                            float* o2) {
-#pragma clang fp contract(off)
-  *o1 = mul_rn(x1, c) + mul_rn(-x2, s);
-  *o2 = mul_rn(x2, c) + mul_rn(x1, s);
-}
-
 // In-place RoPE on x [B, H, L, D]; one thread per (b, h, l, i < D/2).
 template <typename T>
 __global__ void rope_inplace(T* __restrict__ x, const int32_t* __restrict__ pos, int B, int H,

@@ -40,6 +40,27 @@ __device__ __forceinline__ float mul_rn(float a, float b) {
   return p;
 }
 
+// RoPE (MLXRotaryEmbedding / rotate_half, src/ollm/llama_mlx.py:95-182):
+// inv_freq and cos/sin in double rounded once to fp32, angle = fp32(pos *
+// inv_freq), products and sums rounded separately (no FMA).
+__device__ __forceinline__ void rope_cs(int pos, int i, int D, float theta, float* c, float* s) {
+#pragma clang fp contract(off)
+  const float inv = static_cast<float>(1.0 / pow(static_cast<double>(theta),
+                                                 static_cast<double>(2 * i) / D));
+  const float ang = mul_rn(static_cast<float>(pos), inv);
+  double sd, cd;
+  sincos(static_cast<double>(ang), &sd, &cd);
+  *c = static_cast<float>(cd);
+  *s = static_cast<float>(sd);
+}
+
+__device__ __forceinline__ void rotate_pair(float x1, float x2, float c, float s, float* o1,
+                                            float* o2) {
+#pragma clang fp contract(off)
+  *o1 = mul_rn(x1, c) + mul_rn(-x2, s);
+  *o2 = mul_rn(x2, c) + mul_rn(x1, s);
+}
+
 // Element access for the two activation dtypes the library computes with.
 struct bf16_t { uint16_t bits; };
 
