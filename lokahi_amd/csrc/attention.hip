@@ -18,6 +18,9 @@
 //     so every lane owns one query row and all softmax state is in-lane.
 //     Key blocks past the causal limit of the 64-query tile are skipped.
 //   * attn_generic : any other shape (e.g. tiny head dims), one wave per query.
+#include <algorithm>
+#include <cstdlib>
+
 #include "strata_common.h"
 
 namespace {
@@ -58,6 +61,39 @@ __device__ __forceinline__ void load_elems(const T* p, float* out) {
   }
 }
 
+// N consecutive elements of a K or V row held as raw bits (converted to
+// floats only when used), so a pipelined loop can keep the next sweep's
+// loads in flight in few registers.
+template <typename T, int N>
+struct Raw {
+  static constexpr int W = N * (int)sizeof(T) / 4;  // 32-bit words
+  uint32_t u[W];
+  __device__ __forceinline__ void load(const T* p) {
+    if constexpr (W % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < W / 4; ++i) {
+        const uint4 v = reinterpret_cast<const uint4*>(p)[i];
+        u[4 * i] = v.x; u[4 * i + 1] = v.y; u[4 * i + 2] = v.z; u[4 * i + 3] = v.w;
+      }
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2*>(p);
+      u[0] = v.x; u[1] = v.y;
+    }
+  }
+  __device__ __forceinline__ void to_float(float* out) const {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        out[2 * i] = __uint_as_float(u[i] << 16);
+        out[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) out[i] = __uint_as_float(u[i]);
+    }
+  }
+};
+
 // --------------------------------------------------------------- decode (Lq=1)
 // grid (nsplit, Hkv, B), block 256.  Each workgroup reduces one key chunk of
 // one KV head for its G query heads to (m, s, o[D]) per head.  With several
@@ -71,7 +107,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const TQ* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
     int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Hkv, int Lk,
     const int* __restrict__ dlen, int causal, int chunk, int nsplit, float scale, float eps,
-    float* __restrict__ part, TQ* __restrict__ out) {
+    float* __restrict__ part, int* __restrict__ arrive, TQ* __restrict__ out) {
   constexpr int EPL = 16 / sizeof(TK);          // key elements per lane
   constexpr int LPK = D / EPL;                  // lanes per key
   constexpr int KPW = 64 / LPK;                 // keys per wave step
@@ -82,8 +118,35 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / LPK, part_idx = lane % LPK;
   const int e0 = part_idx * EPL;
-  // A graph-replayed decode step reads the current key count from memory;
-  // chunks past it find an empty range and publish s = 0.
+  const int t0 = split * chunk;
+  // Keys [t0, tcap) exist in memory; the first sweep's K/V loads are issued
+  // from that range before the key count is known, so they do not wait for
+  // the count to arrive.
+  const int tcap = min(Lk, t0 + chunk);
+  const TK* kb = k + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  const TV* vb = v + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  // Keys t == sub (mod KPW) of each wave's sweeps: a sweep covers J groups
+  // of KPW consecutive keys per wave (KPW * D * sizeof(TK) contiguous bytes
+  // per group), the 4 waves interleave, consecutive sweeps are 4*KPW*J keys
+  // apart.  Two register sets alternate so the loads of sweep i+1 are in
+  // flight while sweep i is computed.
+  using RK = Raw<TK, EPL>;
+  using RV = Raw<TV, EPL>;
+  RK ka[J], kb2[J];
+  RV va[J], vb2[J];
+  const int sweep = 4 * KPW * J;
+  const int first = t0 + wave * KPW;
+  auto fetch = [&](RK* kr, RV* vr, int base, int tl) {
+#pragma unroll
+    for (int jj = 0; jj < J; ++jj) {
+      const int t = max(min(base + jj * 4 * KPW + sub, tl - 1), 0);  // clamped, masked later
+      kr[jj].load(kb + (int64_t)t * D + e0);
+      vr[jj].load(vb + (int64_t)t * D + e0);
+    }
+  };
+  fetch(ka, va, first, tcap);
+  // A graph-replayed decode step reads the current key count from memory
+  // (Lk is then the captured capacity); chunks past it publish s = 0.
   if (dlen) Lk = *dlen;
 
   int kend = Lk;
@@ -91,11 +154,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const int p = qpos ? qpos[b] : Lk - 1;
     kend = min(Lk, p + 1);
   }
-  const int t0 = split * chunk;
   const int t1 = min(kend, t0 + chunk);
-
-  const TK* kb = k + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
-  const TV* vb = v + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
 
   float qv[G][EPL];
 #pragma unroll
@@ -111,17 +170,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     for (int e = 0; e < EPL; ++e) o[g][e] = 0.f;
   }
 
-  // Wave-uniform loop: each step the wave covers J groups of KPW consecutive
-  // keys (KPW * D * sizeof(TK) contiguous bytes per group); the 4 waves
-  // interleave.  Stream `sub` of a wave always sees keys t == sub (mod KPW).
   const float sl2 = scale * kLog2e;
-  for (int base = t0 + wave * KPW; base < t1; base += 4 * KPW * J) {
+  auto consume = [&](const RK* kr, const RV* vr, int base) {
     float kx[J][EPL], vx[J][EPL];
 #pragma unroll
     for (int jj = 0; jj < J; ++jj) {
-      const int t = min(base + jj * 4 * KPW + sub, t1 - 1);  // clamped, masked below
-      load_elems<TK, EPL>(kb + (int64_t)t * D + e0, kx[jj]);
-      load_elems<TV, EPL>(vb + (int64_t)t * D + e0, vx[jj]);
+      kr[jj].to_float(kx[jj]);
+      vr[jj].to_float(vx[jj]);
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -154,51 +209,122 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         m[g] = mn;
       }
     }
+  };
+  for (int base = first; base < t1; base += 2 * sweep) {
+    if (base + sweep < t1) fetch(kb2, vb2, base + sweep, t1);
+    consume(ka, va, base);
+    if (base + sweep >= t1) break;
+    if (base + 2 * sweep < t1) fetch(ka, va, base + 2 * sweep, t1);
+    consume(kb2, vb2, base + sweep);
   }
 
-  // ---- merge the KPW streams of each wave with shuffles, then the 4 waves in LDS
-  __shared__ float sm_m[4][G], sm_s[4][G];
-  __shared__ float sm_o[4][G][D];
+  // ---- merge the 4*KPW streams of the workgroup in LDS: every stream
+  // (wave, sub) publishes its (m, s, o[D]) per head, then all threads
+  // combine them, GB heads per round.
+  constexpr int NS = 4 * KPW;
+  constexpr int GB = G < 4 ? G : 4;
+  __shared__ float sm_m[NS][GB], sm_s[NS][GB];
+  __shared__ float sm_o[NS][GB][D];
+  const int stream = wave * KPW + sub;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float mw = m[g];
-    for (int off = LPK; off < 64; off <<= 1) mw = fmaxf(mw, __shfl_xor(mw, off, 64));
-    const float f = (s[g] > 0.f) ? exp2f(m[g] - mw) : 0.f;
-    float sw = s[g] * f;
-    for (int off = LPK; off < 64; off <<= 1) sw += __shfl_xor(sw, off, 64);
+  for (int g0 = 0; g0 < G; g0 += GB) {
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      float oe = o[g][e] * f;
-      for (int off = LPK; off < 64; off <<= 1) oe += __shfl_xor(oe, off, 64);
-      if (sub == 0) sm_o[wave][g][e0 + e] = oe;
-    }
-    if (lane == 0) { sm_m[wave][g] = mw; sm_s[wave][g] = sw; }
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-    const int g = idx / D, d = idx - g * D;
-    float mx = -INFINITY;
+    for (int gl = 0; gl < GB; ++gl) {
+      const int g = g0 + gl;
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
-      if (sm_s[w][g] > 0.f) mx = fmaxf(mx, sm_m[w][g]);
-    float ss = 0.f, oo = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      if (sm_s[w][g] > 0.f) {
-        const float f = exp2f(sm_m[w][g] - mx);
-        ss = fmaf(sm_s[w][g], f, ss);
-        oo = fmaf(sm_o[w][g][d], f, oo);
+      for (int e = 0; e < EPL; ++e) sm_o[stream][gl][e0 + e] = o[g][e];
+      if (part_idx == 0) {
+        sm_m[stream][gl] = m[g];
+        sm_s[stream][gl] = s[g];
       }
     }
-    const int hq = hkv * G + g;
-    if (nsplit == 1) {
-      Elem<TQ>::store(out, ((int64_t)b * Hq + hq) * D + d, oo / fmaxf(ss, eps));
-    } else {
-      float* pp = part + (((int64_t)b * Hq + hq) * nsplit + split) * (D + 2);
-      pp[d] = oo;
-      if (d == 0) { pp[D] = mx; pp[D + 1] = ss; }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < GB * D; idx += 256) {
+      const int gl = idx / D, d = idx - gl * D;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NS; ++w)
+        if (sm_s[w][gl] > 0.f) mx = fmaxf(mx, sm_m[w][gl]);
+      float ss = 0.f, oo = 0.f;
+#pragma unroll
+      for (int w = 0; w < NS; ++w) {
+        if (sm_s[w][gl] > 0.f) {
+          const float f = exp2f(sm_m[w][gl] - mx);
+          ss = fmaf(sm_s[w][gl], f, ss);
+          oo = fmaf(sm_o[w][gl][d], f, oo);
+        }
+      }
+      const int hq = hkv * G + g0 + gl;
+      if (nsplit == 1) {
+        Elem<TQ>::store(out, ((int64_t)b * Hq + hq) * D + d, oo / fmaxf(ss, eps));
+      } else {
+        float* pp = part + (((int64_t)b * Hq + hq) * nsplit + split) * (D + 2);
+        pp[d] = oo;
+        if (d == 0) { pp[D] = mx; pp[D + 1] = ss; }
+      }
     }
+    if (g0 + GB < G) __syncthreads();
   }
+  if (nsplit == 1 || arrive == nullptr) return;
+
+  // The last workgroup of this (b, hkv) to finish merges the nsplit partials
+  // of its G heads.  Release: partials are written back device-wide before
+  // the arrival count; acquire: the merger's caches are invalidated after it.
+  __shared__ int s_last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(&arrive[b * Hkv + hkv], 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == nsplit - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  __shared__ float sw[4][kMaxDecodeSplits];
+  for (int g = wave; g < G; g += 4) {
+    const int64_t bh = (int64_t)b * Hq + hkv * G + g;
+    const float* pp = part + bh * nsplit * (D + 2);
+    float mxg = -INFINITY;
+    for (int i = lane; i < nsplit; i += 64) {
+      const float si = pp[(int64_t)i * (D + 2) + D + 1];
+      const float mi = si > 0.f ? pp[(int64_t)i * (D + 2) + D] : -INFINITY;
+      sw[wave][i] = mi;
+      mxg = fmaxf(mxg, mi);
+    }
+    for (int off = 32; off >= 1; off >>= 1) mxg = fmaxf(mxg, __shfl_xor(mxg, off, 64));
+    float st = 0.f;
+    for (int i = lane; i < nsplit; i += 64) {
+      const float w = sw[wave][i] == -INFINITY ? 0.f : exp2f(sw[wave][i] - mxg);
+      sw[wave][i] = w;
+      st = fmaf(pp[(int64_t)i * (D + 2) + D + 1], w, st);
+    }
+    st = wave_sum(st);
+    __builtin_amdgcn_wave_barrier();
+    const float inv = 1.f / fmaxf(st, eps);
+    constexpr int DL = D / 64;  // head-dim entries per lane
+    float oo[DL];
+#pragma unroll
+    for (int c = 0; c < DL; ++c) oo[c] = 0.f;
+    for (int i0 = 0; i0 < nsplit; i0 += 8) {
+      float pv[8][DL];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int c = 0; c < DL; ++c)
+          pv[u][c] = pp[(int64_t)min(i0 + u, nsplit - 1) * (D + 2) + lane + 64 * c];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (i0 + u < nsplit)
+#pragma unroll
+          for (int c = 0; c < DL; ++c) oo[c] = fmaf(pv[u][c], sw[wave][i0 + u], oo[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < DL; ++c) Elem<TQ>::store(out, bh * D + lane + 64 * c, oo[c] * inv);
+  }
+  // ready for the next launch (graph replays reuse the counters)
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&arrive[b * Hkv + hkv], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // grid (B*Hq), block 256: combine the nsplit partials of one (b, hq).  All
@@ -499,9 +625,12 @@ __global__ __launch_bounds__(64) void attn_generic(
 
 // Key-axis split of the decode kernel for `Lcap` keys: enough workgroups to
 // cover the GPU about 4x, at least 64 keys (one 4-wave sweep) per split, at
-// most kMaxDecodeSplits splits.
+// most kMaxDecodeSplits splits.  At batch 1 the kernel is bound by each
+// wave's dependent VALU chain, so short splits (more waves) win
+// (STRATA_ATTN_MIN_CHUNK overrides the minimum).
 void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
-  const int min_chunk = 64;
+  int min_chunk = 64;
+  if (const char* e = getenv("STRATA_ATTN_MIN_CHUNK")) min_chunk = std::max(64, atoi(e));
   int want = (num_cus * 4 + B * Hkv - 1) / (B * Hkv);
   if (want > kMaxDecodeSplits) want = kMaxDecodeSplits;
   int nsplit = (Lcap + min_chunk - 1) / min_chunk;
@@ -536,16 +665,17 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
     }
   }
   dim3 grid(nsplit, Hkv, B);
+  int* arrive = ex.arrive;
 #define STRATA_DEC(GV)                                                                        \
   if (G == GV)                                                                                \
     hipLaunchKernelGGL((attn_decode_kernel<TQ, TK, TV, D, GV>), grid, dim3(256), 0, stream,   \
                        (const TQ*)q, (const TK*)k, (const TV*)v, kv_bs, kv_hs, qpos, Hq, Hkv, \
-                       Lk, ex.dlen, causal, chunk, nsplit, scale, eps, part, (TQ*)out);
+                       Lk, ex.dlen, causal, chunk, nsplit, scale, eps, part, arrive, (TQ*)out);
   STRATA_DEC(1) else STRATA_DEC(2) else STRATA_DEC(4) else STRATA_DEC(8) else
     return strata_set_error(STRATA_ENOTSUP, "decode attention: group size %d not in {1,2,4,8}", G);
 #undef STRATA_DEC
   STRATA_HIP_CHECK(hipGetLastError());
-  if (nsplit > 1) {
+  if (nsplit > 1 && arrive == nullptr) {
     hipLaunchKernelGGL((attn_decode_merge<TQ>), dim3(B * Hq), dim3(256), 0, stream, part, nsplit,
                        D, eps, (TQ*)out);
     STRATA_HIP_CHECK(hipGetLastError());

@@ -5,7 +5,8 @@
 // Follows MLXLlamaForCausalLM.__call__ (src/ollm/llama_mlx.py:863-912),
 // MLXLlamaModel.__call__ (740-833), MLXLlamaDecoderLayer.__call__ (608-658),
 // MLXLlamaAttention.__call__ (220-342), MLXLlamaMLP (345-432) and
-// greedy_generate_mx (src/ollm/generation.py:7-50).  Per layer:
+// greedy_generate_mx (src/ollm/generation.py:7-50).  Per layer of a
+// prefill (the decode step fuses further, see forward_layers):
 //   h <- h + delta;  xn = RMSNorm(h)               (fused residual + norm)
 //   q, k, v = q4(xn)                               (one launch)
 //   RoPE(q, k) at the cache position; append k, v   (one launch)
@@ -18,7 +19,10 @@
 // and a final one-thread kernel records the token and advances the counters.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cstdlib>
 #include <cstring>
+#include <map>
 #include <vector>
 
 #include "strata_internal.h"
@@ -39,9 +43,14 @@ struct strata_decoder {
   int* counters;          // {step, position, key count}
   float* part;            // split-K partials for graph-mode decode attention
   int part_splits;
+  int* arrive;            // split-K arrival counters [max_batch * num_kv_heads] (self-resetting)
+  bool fused_merge;       // merge split-K partials in the attention kernel (else a merge launch)
   void* amax;             // argmax partials [max_batch * kArgmaxBlocks * 8 B]
   hipStream_t stream;     // the decoder's own stream (graph capture / replay)
-  hipGraphExec_t graph;   // captured decode step
+  // Captured decode steps, one per key-capacity bucket: a step at key count
+  // n replays the graph captured for capacity roundup(n, kKeyBucket), so the
+  // split-K attention launch is sized to the context actually in use.
+  std::map<int, hipGraphExec_t> graphs;
   int graph_batch;
   float graph_temp;
   int32_t* graph_out;
@@ -64,9 +73,12 @@ int alloc(void** p, size_t bytes) {
     if (_rc) return _rc;        \
   } while (0)
 
+constexpr int kKeyBucket = 256;
+
 // One decoder forward over T = B*L tokens at positions pos0..pos0+L-1
-// (pos0 < 0: read from counters[1], decode graph mode, L == 1).
-int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream) {
+// (pos0 < 0: read from counters[1], decode graph mode, L == 1, with at most
+// `key_cap` keys per layer).
+int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int key_cap = 0) {
   const strata_llama_config& c = d->cfg;
   const int T = B * L;
   const int H = c.hidden_size, F = c.intermediate_size, D = c.head_dim;
@@ -76,6 +88,51 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream) {
   const bool graph_mode = pos0 < 0;
   // One-token steps (T <= 8 rows) fuse RoPE/append and SiLU into GEMV epilogues.
   const bool decode = L == 1 && T <= 8;
+  if (decode) {
+    // Five launches per layer; the residual stream h is updated in place by
+    // the o/down epilogues, and RMSNorm runs in the q/k/v and gate/up
+    // prologues:
+    //   q, k, v = q4(RMSNorm(h)); RoPE(q, k); append k, v     (one launch)
+    //   a = GQA attention(q, K[:len], V[:len])                 (split-K)
+    //   h = h + q4_o(a)                                        (one launch)
+    //   act = silu(q4_gate(RMSNorm(h))) * q4_up(RMSNorm(h))    (one launch)
+    //   h = h + q4_down(act)                                   (one launch)
+    for (int li = 0; li < c.num_layers; ++li) {
+      const strata_llama_layer& Lw = d->layers[li];
+      void* kc = kv->kl(li);
+      void* vc = kv->vl(li);
+      strata_q4_weight qkv[3] = {Lw.q, Lw.k, Lw.v};
+      GemvEpilogue eq{2, D, Hq, Hkv, kv->Lmax, graph_mode ? 0 : pos0,
+                      graph_mode ? d->counters + 1 : nullptr, c.rope_theta,
+                      (uint16_t*)d->qr, (uint16_t*)kc, (uint16_t*)vc, Lw.input_norm,
+                      c.rms_norm_eps};
+      RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, qkv, 3, eq, stream));
+      AttnExtra ex;
+      ex.part = d->part;
+      ex.part_splits = d->part_splits;
+      ex.arrive = d->fused_merge ? d->arrive : nullptr;
+      if (graph_mode) ex.dlen = d->counters + 2;
+      RC(strata_attention_dispatch(d->ctx, d->qr, STRATA_BF16, kc, STRATA_BF16, vc, STRATA_BF16,
+                                   kv_bs, kv_hs, nullptr, B, Hq, Hkv, 1,
+                                   graph_mode ? key_cap : pos0 + 1, D, 1, 1e-12f, d->attn, ex,
+                                   stream));
+      GemvEpilogue er{3, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr, nullptr, 0.f};
+      strata_q4_weight o = Lw.o;
+      o.y = d->h;
+      RC(strata_q4_gemv_epi(d->ctx, d->attn, T, Hq * D, &o, 1, er, stream));
+      strata_q4_weight gu[2] = {Lw.gate, Lw.up};
+      gu[0].y = d->act;
+      GemvEpilogue es{1, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr, Lw.post_norm,
+                      c.rms_norm_eps};
+      RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, gu, 2, es, stream));
+      strata_q4_weight dn = Lw.down;
+      dn.y = d->h;
+      RC(strata_q4_gemv_epi(d->ctx, d->act, T, F, &dn, 1, er, stream));
+    }
+    RC(strata_rmsnorm_launch(d->h, nullptr, d->final_norm, T, H, c.rms_norm_eps, d->hn, stream));
+    return strata_bf16_gemv(d->ctx, d->hn, B, H, d->lm_head, c.vocab_size, d->logits, STRATA_F32,
+                            stream);
+  }
   for (int li = 0; li < c.num_layers; ++li) {
     const strata_llama_layer& Lw = d->layers[li];
     RC(strata_rmsnorm_launch(d->h, li == 0 ? nullptr : d->delta, Lw.input_norm, T, H,
@@ -86,59 +143,33 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream) {
     qkv[2].y = d->v;
     void* kc = kv->kl(li);
     void* vc = kv->vl(li);
-    if (decode) {
-      // q/k/v GEMV whose epilogue applies RoPE and appends k, v to the cache
-      GemvEpilogue e{2, D, Hq, Hkv, kv->Lmax, graph_mode ? 0 : pos0,
-                     graph_mode ? d->counters + 1 : nullptr, c.rope_theta,
-                     (uint16_t*)d->qr, (uint16_t*)kc, (uint16_t*)vc};
-      RC(strata_q4_gemv_epi(d->ctx, d->xn, T, H, qkv, 3, e, stream));
-    } else {
-      for (auto& w : qkv)
-        RC(strata_q4_gemm_launch(d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
-                                 stream));
-      RC(strata_rope_kv_fused_launch(d->q, d->k, d->v, STRATA_BF16, B, Hq, Hkv, L, D, kv->Lmax,
-                                     pos0, nullptr, c.rope_theta, d->qr, kc, vc, STRATA_BF16,
-                                     stream));
-    }
+    for (auto& w : qkv)
+      RC(strata_q4_gemm_launch(d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
+                               stream));
+    RC(strata_rope_kv_fused_launch(d->q, d->k, d->v, STRATA_BF16, B, Hq, Hkv, L, D, kv->Lmax,
+                                   pos0, nullptr, c.rope_theta, d->qr, kc, vc, STRATA_BF16,
+                                   stream));
     AttnExtra ex;
-    if (graph_mode) {
-      ex.dlen = d->counters + 2;
-      ex.part = d->part;
-      ex.part_splits = d->part_splits;
-      RC(strata_attention_dispatch(d->ctx, d->qr, STRATA_BF16, kc, STRATA_BF16, vc, STRATA_BF16,
-                                   kv_bs, kv_hs, nullptr, B, Hq, Hkv, 1, kv->Lmax, D, 1, 1e-12f,
-                                   d->attn, ex, stream));
-    } else {
-      ex.out_tm = 1;  // prefill writes [B, L, Hq, D], the o_proj input layout
-      RC(strata_attention_dispatch(d->ctx, d->qr, STRATA_BF16, kc, STRATA_BF16, vc, STRATA_BF16,
-                                   kv_bs, kv_hs, nullptr, B, Hq, Hkv, L, pos0 + L, D, 1, 1e-12f,
-                                   d->attn, ex, stream));
-    }
+    ex.out_tm = 1;  // prefill writes [B, L, Hq, D], the o_proj input layout
+    RC(strata_attention_dispatch(d->ctx, d->qr, STRATA_BF16, kc, STRATA_BF16, vc, STRATA_BF16,
+                                 kv_bs, kv_hs, nullptr, B, Hq, Hkv, L, pos0 + L, D, 1, 1e-12f,
+                                 d->attn, ex, stream));
     strata_q4_weight o = Lw.o;
     o.y = d->o;
-    if (decode) RC(strata_q4_gemv(d->ctx, d->attn, STRATA_BF16, T, Hq * D, &o, 1, STRATA_BF16, stream));
-    else RC(strata_q4_gemm_launch(d->attn, T, Hq * D, o.w, o.scales, o.biases, (int)o.N, o.y,
-                                  STRATA_BF16, stream));
+    RC(strata_q4_gemm_launch(d->attn, T, Hq * D, o.w, o.scales, o.biases, (int)o.N, o.y,
+                             STRATA_BF16, stream));
     RC(strata_rmsnorm_launch(d->h, d->o, Lw.post_norm, T, H, c.rms_norm_eps, d->xn, stream));
     strata_q4_weight gu[2] = {Lw.gate, Lw.up};
     gu[0].y = d->gate;
     gu[1].y = d->up;
-    if (decode) {
-      // gate/up GEMV whose epilogue writes silu(gate) * up
-      gu[0].y = d->act;
-      GemvEpilogue e{1, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr};
-      RC(strata_q4_gemv_epi(d->ctx, d->xn, T, H, gu, 2, e, stream));
-    } else {
-      for (auto& w : gu)
-        RC(strata_q4_gemm_launch(d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
-                                 stream));
-      RC(strata_silu_mul_launch(d->gate, d->up, (int64_t)T * F, d->act, stream));
-    }
+    for (auto& w : gu)
+      RC(strata_q4_gemm_launch(d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
+                               stream));
+    RC(strata_silu_mul_launch(d->gate, d->up, (int64_t)T * F, d->act, stream));
     strata_q4_weight dn = Lw.down;
     dn.y = d->delta;
-    if (decode) RC(strata_q4_gemv(d->ctx, d->act, STRATA_BF16, T, F, &dn, 1, STRATA_BF16, stream));
-    else RC(strata_q4_gemm_launch(d->act, T, F, dn.w, dn.scales, dn.biases, (int)dn.N, dn.y,
-                                  STRATA_BF16, stream));
+    RC(strata_q4_gemm_launch(d->act, T, F, dn.w, dn.scales, dn.biases, (int)dn.N, dn.y,
+                             STRATA_BF16, stream));
   }
   // final norm of h + delta, then lm_head on the last position of each row
   RC(strata_rmsnorm_launch(d->h, d->delta, d->final_norm, T, H, c.rms_norm_eps, d->hn, stream));
@@ -212,6 +243,10 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
   d->kv = kv;
   d->max_batch = max_batch;
   d->max_tokens = max_tokens;
+  // The in-kernel merge (last arriving workgroup, device-scope fences) is
+  // slower on MI355X than a separate merge launch; STRATA_ATTN_FUSED_MERGE
+  // enables it.
+  d->fused_merge = getenv("STRATA_ATTN_FUSED_MERGE") != nullptr;
   const size_t T = max_tokens;
   const size_t H = c.hidden_size, F = c.intermediate_size, QW = (size_t)c.num_heads * c.head_dim,
                KW = (size_t)c.num_kv_heads * c.head_dim;
@@ -226,6 +261,7 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
       {reinterpret_cast<void**>(&d->ids), (size_t)max_batch * 4},
       {reinterpret_cast<void**>(&d->counters), 16},
       {&d->amax, (size_t)max_batch * kArgmaxBlocks * 8},
+      {reinterpret_cast<void**>(&d->arrive), (size_t)max_batch * c.num_kv_heads * 4},
   };
   for (auto& b : bufs)
     if (!rc) rc = alloc(b.p, b.bytes);
@@ -233,6 +269,8 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
   if (!rc)
     rc = alloc(reinterpret_cast<void**>(&d->part),
                (size_t)kv->B * c.num_heads * d->part_splits * (c.head_dim + 2) * 4);
+  if (!rc && hipMemset(d->arrive, 0, (size_t)max_batch * c.num_kv_heads * 4) != hipSuccess)
+    rc = strata_set_error(STRATA_EHIP, "decoder: counter initialisation failed");
   if (!rc && hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess)
     rc = strata_set_error(STRATA_EHIP, "decoder: stream creation failed");
   if (rc) {
@@ -246,9 +284,9 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
 int strata_decoder_destroy(strata_decoder* d) {
   if (!d) return STRATA_OK;
   hipDeviceSynchronize();
-  if (d->graph) hipGraphExecDestroy(d->graph);
+  for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
   void* ptrs[] = {d->h, d->xn, d->q, d->k, d->v, d->qr, d->attn, d->o, d->gate, d->up, d->act,
-                  d->delta, d->hn, d->logits, d->ids, d->counters, d->part, d->amax};
+                  d->delta, d->hn, d->logits, d->ids, d->counters, d->part, d->amax, d->arrive};
   for (void* p : ptrs)
     if (p) hipFree(p);
   if (d->stream) hipStreamDestroy(d->stream);
@@ -298,43 +336,51 @@ int strata_decoder_generate(strata_decoder* d, const int32_t* prompt, int B, int
   STRATA_HIP_CHECK(hipMemcpyAsync(d->counters, init, sizeof(init), hipMemcpyHostToDevice, s));
   RC(strata_decode_advance_launch(d->ids, B, out_tokens, max_new, d->counters, s));
 
-  auto decode_step = [&](hipStream_t st) -> int {
+  auto decode_step = [&](hipStream_t st, int key_cap) -> int {
     RC(strata_embed_launch(d->embed, c.vocab_size, c.hidden_size, d->ids, B, d->h, st));
-    RC(forward_layers(d, B, 1, -1, st));
+    RC(forward_layers(d, B, 1, -1, st, key_cap));
     RC(strata_argmax_launch(d->logits, B, c.vocab_size, temperature, d->ids, d->amax, st));
     RC(strata_decode_advance_launch(d->ids, B, out_tokens, max_new, d->counters, st));
     return STRATA_OK;
   };
   if (max_new > 1) {
-    if (use_graph) {
-      const bool reuse = d->graph && d->graph_batch == B && d->graph_temp == temperature &&
-                         d->graph_out == out_tokens && d->graph_out_stride == max_new;
-      if (!reuse) {
-        if (d->graph) {
-          STRATA_HIP_CHECK(hipGraphExecDestroy(d->graph));
-          d->graph = nullptr;
-        }
+    const bool reuse = d->graph_batch == B && d->graph_temp == temperature &&
+                       d->graph_out == out_tokens && d->graph_out_stride == max_new;
+    if (!reuse) {
+      for (auto& kvp : d->graphs) STRATA_HIP_CHECK(hipGraphExecDestroy(kvp.second));
+      d->graphs.clear();
+      d->graph_batch = B;
+      d->graph_temp = temperature;
+      d->graph_out = out_tokens;
+      d->graph_out_stride = max_new;
+    }
+    for (int i = 1; i < max_new; ++i) {
+      // step i feeds the token at position pos0 + L + i - 1: that many keys + 1
+      const int keys = pos0 + L + i;
+      const int cap = std::min(d->kv->Lmax, (keys + kKeyBucket - 1) / kKeyBucket * kKeyBucket);
+      if (!use_graph) {
+        RC(decode_step(s, cap));
+        continue;
+      }
+      auto it = d->graphs.find(cap);
+      if (it == d->graphs.end()) {
         hipGraph_t g;
+        hipGraphExec_t ge = nullptr;
         STRATA_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-        const int crc = decode_step(s);
+        const int crc = decode_step(s, cap);
         const hipError_t ce = hipStreamEndCapture(s, &g);
         if (crc) return crc;
         if (ce != hipSuccess)
           return strata_set_error(STRATA_EHIP, "decode graph capture failed: %s",
                                   hipGetErrorString(ce));
-        const hipError_t ie = hipGraphInstantiate(&d->graph, g, nullptr, nullptr, 0);
+        const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
         hipGraphDestroy(g);
         if (ie != hipSuccess)
           return strata_set_error(STRATA_EHIP, "decode graph instantiation failed: %s",
                                   hipGetErrorString(ie));
-        d->graph_batch = B;
-        d->graph_temp = temperature;
-        d->graph_out = out_tokens;
-        d->graph_out_stride = max_new;
+        it = d->graphs.emplace(cap, ge).first;
       }
-      for (int i = 1; i < max_new; ++i) STRATA_HIP_CHECK(hipGraphLaunch(d->graph, s));
-    } else {
-      for (int i = 1; i < max_new; ++i) RC(decode_step(s));
+      STRATA_HIP_CHECK(hipGraphLaunch(it->second, s));
     }
   }
   STRATA_HIP_CHECK(hipEventRecord(ev, s));

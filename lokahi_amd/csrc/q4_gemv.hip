@@ -1,649 +1,20 @@
-// Decode-side quantized (q4 affine, group 64) and bf16 matrix-vector kernels.
-//
-// y[m, n] = sum_k x[m, k] * (s[n, k/64] * q[n, k] + b[n, k/64])
-// (mx.quantized_matmul(transpose=True), src/ollm/llama_mlx.py:53-74)
-//
-// Design (HBM-bound streaming, gfx950 wave64):
-//   * x for MT batch rows is staged once per workgroup into LDS, already
-//     rearranged into bf16 pairs (x[8j+c], x[8j+c+4]) so that one AND-OR of a
-//     packed word with the magic 0x43004300 yields the matching bf16 pair
-//     (128+q[8j+c], 128+q[8j+c+4]) exactly; v_dot2_f32_bf16 then accumulates
-//     x*(128+q) in fp32.  Per 32-element half group the offset is removed
-//     with the precomputed LDS sum X = sum x:
-//         acc += s * D + (b - 128 s) * X
-//   * every lane streams one 16-byte uint4 (32 codes) per row per step, so a
-//     wave reads 1 KiB contiguous per row per step (fully coalesced), R rows
-//     at once to keep R*16 B per lane in flight and reuse the x reads;
-//   * one workgroup per row block; every lane issues all of its weight loads
-//     for a K chunk before it touches LDS, so thousands of waves keep the HBM
-//     queues full; several linears that share x (q/k/v, gate/up) are one
-//     launch ("problems" concatenated by row).
-//   * lanes reduce with xor-butterflies at the end; results are deterministic.
-#include <cstdlib>
-
-#include "strata_internal.h"
-
-namespace {
-
-constexpr int kMaxProblems = 8;
-constexpr uint32_t kMagicPair = 0x43004300u;  // bf16 (128.0, 128.0)
-
-struct Q4Problem {
-  const uint4* w;      // [n, K/32] uint4  (== uint32 [n, K/8])
-  const uint16_t* s;   // [n, K/64] bf16
-  const uint16_t* b;   // [n, K/64] bf16
-  void* y;             // [M, n]
-  int n;
-  int row0;
-};
-
-// Epilogues (decode engine), chosen by Q4Batch::epi:
-//   EPI_STORE     : y[m, n] = bf16/fp32(acc)
-//   EPI_SILU_PAIR : problems 0/1 = gate/up with rows interleaved (row 2n is
-//                   gate n, row 2n+1 is up n, both in one wave); writes
-//                   y0[m, n] = bf16(silu(bf16(gate)) * bf16(up))
-//                   (llama_mlx.py:399-407) - the gate/up outputs never
-//                   leave registers;
-//   EPI_ROPE_KV   : problems 0/1/2 = q/k/v; inside each head the rows are
-//                   ordered (0, D/2, 1, D/2+1, ...) so a wave holds a RoPE
-//                   pair; writes rotated q head-major to q_out, rotated k and
-//                   v into the KV cache at the step's position
-//                   (llama_mlx.py:271-297; values are rounded to bf16 before
-//                   RoPE, as the separate kernels do).
-enum { EPI_STORE = 0, EPI_SILU_PAIR = 1, EPI_ROPE_KV = 2 };
-
-struct Q4Batch {
-  Q4Problem p[kMaxProblems];
-  int count;
-  int total_rows;
-  int epi;
-  // EPI_ROPE_KV
-  int head_dim, n_heads, n_kv_heads, lmax, pos0;
-  const int* dpos;  // device position (graph-replayed step) or nullptr
-  float theta;
-  uint16_t* q_out;  // [M, Hq, 1, D] bf16
-  uint16_t* kc;     // cache layer [M, Hkv, lmax, D] bf16
-  uint16_t* vc;
-};
-
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
-template <typename YT>
-__device__ __forceinline__ void store_y(void* y, int64_t idx, float v) {
-  Elem<YT>::store(reinterpret_cast<YT*>(y), idx, v);
-}
-
-// Stage MT rows of x (bf16 or f32) into LDS.
-//   bf16: xq[(mm*4 + j) * nv + i] = uint4 of the 4 bf16 pairs of word 4i+j,
-//         xs[mm * nv + i]         = sum of the 32 x values of uint4 i.
-//   f32 : xf[(mm*8 + c) * nv + i] = float4 of elements 32i+4c .. 32i+4c+3,
-//         xs as above.
-template <typename XT, int MT>
-__device__ __forceinline__ void stage_x(const XT* __restrict__ x, int M, int K, int m0,
-                                        uint4* smem, int nv) {
-  float* xs;
-  if constexpr (sizeof(XT) == 2) {
-    uint4* xq = smem;
-    xs = reinterpret_cast<float*>(smem + MT * 4 * nv);
-    for (int idx = threadIdx.x; idx < MT * nv; idx += blockDim.x) {
-      const int mm = idx / nv, i = idx - mm * nv;
-      const int m = m0 + mm;
-      float sum = 0.f;
-      // rows past M read row M-1 (in bounds) and are zeroed after the loads
-      const uint4* xr = reinterpret_cast<const uint4*>(x) + ((int64_t)min(m, M - 1) * K + (int64_t)i * 32) / 8;
-      uint4 vv[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) vv[j] = xr[j];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint4 v = m < M ? vv[j] : make_uint4(0, 0, 0, 0);
-        uint4 pr;
-        pr.x = (v.x & 0xffffu) | (v.z << 16);
-        pr.y = (v.x >> 16) | (v.z & 0xffff0000u);
-        pr.z = (v.y & 0xffffu) | (v.w << 16);
-        pr.w = (v.y >> 16) | (v.w & 0xffff0000u);
-        xq[(mm * 4 + j) * nv + i] = pr;
-        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          sum += __uint_as_float(u[c] << 16) + __uint_as_float(u[c] & 0xffff0000u);
-      }
-      xs[mm * nv + i] = sum;
-    }
-  } else {
-    float4* xf = reinterpret_cast<float4*>(smem);
-    xs = reinterpret_cast<float*>(smem + MT * 8 * nv);
-    for (int idx = threadIdx.x; idx < MT * nv; idx += blockDim.x) {
-      const int mm = idx / nv, i = idx - mm * nv;
-      const int m = m0 + mm;
-      float sum = 0.f;
-      const float4* xr = reinterpret_cast<const float4*>(x + (int64_t)m * K + (int64_t)i * 32);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (m < M) v = xr[c];
-        xf[(mm * 8 + c) * nv + i] = v;
-        sum += (v.x + v.y) + (v.z + v.w);
-      }
-      xs[mm * nv + i] = sum;
-    }
-  }
-}
-
-// One workgroup = NW waves, persistent over row blocks (grid-stride).  x is
-// staged into LDS once per workgroup behind the only barrier; after that each
-// wave streams its rows with no synchronization: per row block it issues all
-// R*U 16-byte weight loads (and their scales/biases, held in full 32-bit
-// registers so no load waits on another), then computes.  The wave index is
-// made wave-uniform (readfirstlane) so row/problem bookkeeping is scalar.
-// bf16 x staging split in two so its global loads can be issued before the
-// weight loads and written to LDS after them.  Thread t owns x items
-// t, t + blockDim.x (XI of them); an item is the 32 x values of one weight
-// uint4 position i of batch row mm.
-template <int MT, int XI>
-struct XStage {
-  uint4 v[XI][4];
-};
-
-template <int MT, int XI>
-__device__ __forceinline__ void xstage_load(XStage<MT, XI>& st, const uint16_t* __restrict__ x,
-                                            int M, int K, int m0, int nv) {
-#pragma unroll
-  for (int k = 0; k < XI; ++k) {
-    const int idx = min((int)(threadIdx.x + k * blockDim.x), MT * nv - 1);
-    const int mm = idx / nv, i = idx - mm * nv;
-    const int m = min(m0 + mm, M - 1);  // rows past M are zeroed at store time
-    const uint4* xr = reinterpret_cast<const uint4*>(x + (int64_t)m * K + (int64_t)i * 32);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) st.v[k][j] = xr[j];
-  }
-}
-
-template <int MT, int XI>
-__device__ __forceinline__ void xstage_store(const XStage<MT, XI>& st, int M, int m0, int nv,
-                                             uint4* smem) {
-  uint4* xq = smem;
-  float* xs = reinterpret_cast<float*>(smem + MT * 4 * nv);
-#pragma unroll
-  for (int k = 0; k < XI; ++k) {
-    const int idx = threadIdx.x + k * blockDim.x;
-    if (idx >= MT * nv) break;
-    const int mm = idx / nv, i = idx - mm * nv;
-    const bool live = m0 + mm < M;
-    float sum = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint4 v = live ? st.v[k][j] : make_uint4(0, 0, 0, 0);
-      uint4 pr;
-      pr.x = (v.x & 0xffffu) | (v.z << 16);
-      pr.y = (v.x >> 16) | (v.z & 0xffff0000u);
-      pr.z = (v.y & 0xffffu) | (v.w << 16);
-      pr.w = (v.y >> 16) | (v.w & 0xffff0000u);
-      xq[(mm * 4 + j) * nv + i] = pr;
-      const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        sum += __uint_as_float(u[c] << 16) + __uint_as_float(u[c] & 0xffff0000u);
-    }
-    xs[mm * nv + i] = sum;
-  }
-}
-
-// One workgroup = NW waves = one block of NW*R rows; wave w owns R rows.
-// Order of work: x loads, then every weight/scale/bias load of the first K
-// chunk (16-byte non-temporal loads, unconditional with clamped in-bounds
-// addresses so none sits behind a branch), then x is written to LDS while the
-// weights are still in flight, one barrier, the math, the store.  XI > 0
-// selects that split staging (bf16 x); XI == 0 stages x up front (fp32 x).
-template <int NW, int R, int U, int MT, int XI, typename XT, typename YT>
-__global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
-                                                          Q4Batch batch) {
-  extern __shared__ uint4 smem[];
-  const int nv = K >> 5;  // uint4 (32 codes) per weight row
-  const int m0 = blockIdx.y * MT;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const float* xs = reinterpret_cast<const float*>(smem + MT * (sizeof(XT) == 2 ? 4 : 8) * nv);
-
-  const uint4* wp[R];
-  const uint16_t* sp[R];
-  const uint16_t* bp[R];
-  int pid[R], nloc[R];
-  bool valid[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int row = (blockIdx.x * NW + wave) * R + r;
-    valid[r] = row < batch.total_rows;
-    int pi = 0, n = 0;
-    if (batch.epi == EPI_SILU_PAIR) {
-      pi = row & 1;
-      n = valid[r] ? row >> 1 : 0;
-    } else {
-#pragma unroll
-      for (int t = 1; t < kMaxProblems; ++t)
-        if (t < batch.count && row >= batch.p[t].row0) pi = t;
-      n = valid[r] ? row - batch.p[pi].row0 : 0;
-      if (batch.epi == EPI_ROPE_KV) {  // (h, 2p + w) -> h*D + p + w*D/2
-        const int D = batch.head_dim, j = n % D;
-        n = n - j + (j >> 1) + (j & 1) * (D >> 1);
-      }
-    }
-    pid[r] = pi;
-    nloc[r] = n;
-    wp[r] = batch.p[pi].w + (int64_t)n * nv;
-    sp[r] = batch.p[pi].s + (int64_t)n * (nv >> 1);
-    bp[r] = batch.p[pi].b + (int64_t)n * (nv >> 1);
-  }
-
-  uint4 wv[R][U];
-  uint32_t sv[R][U], bv[R][U];
-  auto issue = [&](int c0) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int ic = min(c0 + lane + 64 * u, nv - 1);
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        wv[r][u] = load_nt(wp[r] + ic);
-        sv[r][u] = sp[r][ic >> 1];
-        bv[r][u] = bp[r][ic >> 1];
-      }
-    }
-  };
-
-  float acc[R][MT];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int mm = 0; mm < MT; ++mm) acc[r][mm] = 0.f;
-
-  auto compute = [&](int c0) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      // A tail lane read a valid slot; zero scale and bias remove it.
-      const bool tail = c0 + lane + 64 * u >= nv;
-      const int i = min(c0 + lane + 64 * u, nv - 1);
-#pragma unroll
-      for (int mm = 0; mm < MT; ++mm) {
-        const float xsum = xs[mm * nv + i];
-        if constexpr (sizeof(XT) == 2) {
-          const uint4* xq = smem;
-          uint4 xa[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) xa[j] = xq[(mm * 4 + j) * nv + i];
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            const uint32_t ww[4] = {wv[r][u].x, wv[r][u].y, wv[r][u].z, wv[r][u].w};
-            float d = 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const uint32_t w = ww[j];
-              d = dot2_bf16((w & 0x000f000fu) | kMagicPair, xa[j].x, d);
-              d = dot2_bf16(((w >> 4) & 0x000f000fu) | kMagicPair, xa[j].y, d);
-              d = dot2_bf16(((w >> 8) & 0x000f000fu) | kMagicPair, xa[j].z, d);
-              d = dot2_bf16(((w >> 12) & 0x000f000fu) | kMagicPair, xa[j].w, d);
-            }
-            const float sc = tail ? 0.f : __uint_as_float(sv[r][u] << 16);
-            const float bc = tail ? 0.f : __uint_as_float(bv[r][u] << 16);
-            acc[r][mm] = fmaf(sc, d, acc[r][mm]);
-            acc[r][mm] = fmaf(fmaf(-128.f, sc, bc), xsum, acc[r][mm]);
-          }
-        } else {
-          const float4* xf = reinterpret_cast<const float4*>(smem);
-          float4 xa[8];
-#pragma unroll
-          for (int c = 0; c < 8; ++c) xa[c] = xf[(mm * 8 + c) * nv + i];
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            const uint32_t ww[4] = {wv[r][u].x, wv[r][u].y, wv[r][u].z, wv[r][u].w};
-            float d = 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const uint32_t lo = ww[j] & 0x0f0f0f0fu;         // codes 0,2,4,6
-              const uint32_t hi = (ww[j] >> 4) & 0x0f0f0f0fu;  // codes 1,3,5,7
-              const float4 xa0 = xa[2 * j], xa1 = xa[2 * j + 1];
-              d = fmaf(xa0.x, (float)(lo & 0xff), d);
-              d = fmaf(xa0.y, (float)(hi & 0xff), d);
-              d = fmaf(xa0.z, (float)((lo >> 8) & 0xff), d);
-              d = fmaf(xa0.w, (float)((hi >> 8) & 0xff), d);
-              d = fmaf(xa1.x, (float)((lo >> 16) & 0xff), d);
-              d = fmaf(xa1.y, (float)((hi >> 16) & 0xff), d);
-              d = fmaf(xa1.z, (float)(lo >> 24), d);
-              d = fmaf(xa1.w, (float)(hi >> 24), d);
-            }
-            const float sc = tail ? 0.f : __uint_as_float(sv[r][u] << 16);
-            const float bc = tail ? 0.f : __uint_as_float(bv[r][u] << 16);
-            acc[r][mm] = fmaf(sc, d, acc[r][mm]);
-            acc[r][mm] = fmaf(bc, xsum, acc[r][mm]);
-          }
-        }
-      }
-    }
-  };
-
-  if constexpr (XI > 0) {
-    XStage<MT, XI> st;
-    xstage_load<MT, XI>(st, reinterpret_cast<const uint16_t*>(x), M, K, m0, nv);
-    issue(0);
-    __builtin_amdgcn_sched_barrier(0);
-    xstage_store<MT, XI>(st, M, m0, nv, smem);
-  } else {
-    stage_x<XT, MT>(x, M, K, m0, smem, nv);
-    issue(0);
-  }
-  __syncthreads();
-  compute(0);
-  for (int c0 = 64 * U; c0 < nv; c0 += 64 * U) {
-    issue(c0);
-    compute(c0);
-  }
-
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int mm = 0; mm < MT; ++mm) acc[r][mm] = wave_sum(acc[r][mm]);
-  if constexpr (R == 2) {
-    if (batch.epi != EPI_STORE) {
-#pragma unroll
-      for (int mm = 0; mm < MT; ++mm) {
-        const int m = m0 + mm;
-        if (lane != mm || !valid[0] || m >= M) continue;
-        const float a0 = bf16_to_f32(f32_to_bf16(acc[0][mm]));
-        const float a1 = bf16_to_f32(f32_to_bf16(acc[1][mm]));
-        if (batch.epi == EPI_SILU_PAIR) {
-          const float sg = a0 / (1.0f + expf(-a0));
-          const Q4Problem& p = batch.p[0];
-          store_y<bf16_t>(p.y, (int64_t)m * p.n + nloc[0], mul_rn(sg, a1));
-        } else {
-          const int D = batch.head_dim, half = D >> 1;
-          const int h = nloc[0] / D, i = nloc[0] - h * D;  // i < D/2: pair (i, i + D/2)
-          const int pos = batch.dpos ? *batch.dpos : batch.pos0;
-          if (pid[0] == 2) {  // v: copy into the cache
-            const int64_t co = (((int64_t)m * batch.n_kv_heads + h) * batch.lmax + pos) * D;
-            batch.vc[co + i] = f32_to_bf16(a0);
-            batch.vc[co + i + half] = f32_to_bf16(a1);
-          } else {
-            float c, sn, o1, o2;
-            rope_cs(pos, i, D, batch.theta, &c, &sn);
-            rotate_pair(a0, a1, c, sn, &o1, &o2);
-            if (pid[0] == 0) {
-              const int64_t qo = ((int64_t)m * batch.n_heads + h) * D;
-              batch.q_out[qo + i] = f32_to_bf16(o1);
-              batch.q_out[qo + i + half] = f32_to_bf16(o2);
-            } else {
-              const int64_t co = (((int64_t)m * batch.n_kv_heads + h) * batch.lmax + pos) * D;
-              batch.kc[co + i] = f32_to_bf16(o1);
-              batch.kc[co + i + half] = f32_to_bf16(o2);
-            }
-          }
-        }
-      }
-      return;
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int mm = 0; mm < MT; ++mm) {
-      const int m = m0 + mm;
-      if (lane == r * MT + mm && valid[r] && m < M) {
-        const Q4Problem& p = batch.p[pid[r]];
-        store_y<YT>(p.y, (int64_t)m * p.n + nloc[r], acc[r][mm]);
-      }
-    }
-}
-
-// Dense bf16-weight GEMV (lm_head): y[m,n] = sum_k x[m,k] * W[n,k]; same
-// load-first structure, one uint4 = 8 weights per lane per step.
-template <int NW, int R, int U, int MT, typename YT>
-__global__ __launch_bounds__(NW * 64) void bf16_gemv_kernel(const uint16_t* __restrict__ x, int M,
-                                                            int K, const uint4* __restrict__ w,
-                                                            int N, YT* __restrict__ y) {
-  extern __shared__ uint4 smem[];
-  const int nv = K >> 3;  // uint4 (8 bf16) per row
-  const int m0 = blockIdx.y * MT;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int row0 = (blockIdx.x * NW + wave) * R;
-  float acc[R][MT];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int mm = 0; mm < MT; ++mm) acc[r][mm] = 0.f;
-  for (int c0 = 0; c0 < nv; c0 += 64 * U) {
-    uint4 wv[R][U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = c0 + lane + 64 * u;
-      const int ic = min(i, nv - 1);
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        // unconditional, clamped load; rows past N are computed but never stored
-        const uint4 t = load_nt(w + (int64_t)min(row0 + r, N - 1) * nv + ic);
-        wv[r][u] = i < nv ? t : make_uint4(0, 0, 0, 0);
-      }
-    }
-    if (c0 == 0) {
-      for (int idx = threadIdx.x; idx < MT * nv; idx += blockDim.x) {
-        const int mm = idx / nv, i = idx - mm * nv;
-        const int m = m0 + mm;
-        smem[idx] = (m < M) ? reinterpret_cast<const uint4*>(x + (int64_t)m * K)[i]
-                            : make_uint4(0, 0, 0, 0);
-      }
-      __syncthreads();
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = min(c0 + lane + 64 * u, nv - 1);
-#pragma unroll
-      for (int mm = 0; mm < MT; ++mm) {
-        const uint4 xa = smem[mm * nv + i];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          float d = acc[r][mm];
-          d = dot2_bf16(wv[r][u].x, xa.x, d);
-          d = dot2_bf16(wv[r][u].y, xa.y, d);
-          d = dot2_bf16(wv[r][u].z, xa.z, d);
-          d = dot2_bf16(wv[r][u].w, xa.w, d);
-          acc[r][mm] = d;
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int mm = 0; mm < MT; ++mm) acc[r][mm] = wave_sum(acc[r][mm]);
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int mm = 0; mm < MT; ++mm) {
-      const int m = m0 + mm;
-      if (lane == r * MT + mm && row0 + r < N && m < M)
-        Elem<YT>::store(y, (int64_t)m * N + row0 + r, acc[r][mm]);
-    }
-}
-
-// Launch geometry of one GEMV: waves per workgroup, rows per wave, uint4 per
-// lane per row per K chunk, batch rows per pass.
-struct GemvShape {
-  int nw, r, u, mt;
-};
-
-// Pick the geometry for `rows` output rows of `nv` uint4 each.  Aim: each
-// lane holds ~8 outstanding 16-byte weight loads (R*U ~ 8) and the launch has
-// several thousand waves; large-K rows use 8-wave workgroups so the x staged
-// in LDS is shared by more rows.
-GemvShape pick_shape(int nv, int rows, int M) {
-  // Measured on MI355X (rocprof / back-to-back launches, weights cycled past
-  // the 256 MB last-level cache): K=4096 rows prefer 4 waves x 2 rows with
-  // U=2, small launches 8 waves x 1 row; K=14336 prefers 8 waves x 1 row, U=7.
-  GemvShape g;
-  const int chunks = (nv + 63) / 64;
-  g.u = chunks <= 2 ? 2 : (chunks <= 4 ? 4 : (chunks <= 7 ? 7 : 8));
-  g.mt = M >= 4 ? 4 : (M >= 2 ? 2 : 1);
-  if (g.mt > 1) {
-    g.r = 2;
-    g.nw = 4;
-  } else if (g.u == 2) {
-    g.nw = rows < 8192 ? 8 : 4;
-    g.r = rows < 8192 ? 1 : 2;
-  } else {
-    g.nw = g.u == 4 ? 4 : 8;
-    g.r = 1;
-  }
-  if (const char* e = getenv("STRATA_GEMV_NW")) g.nw = atoi(e);
-  if (const char* e = getenv("STRATA_GEMV_R")) g.r = atoi(e);
-  if (const char* e = getenv("STRATA_GEMV_U")) g.u = atoi(e);
-  return g;
-}
-
-template <int NW, int R, int U, int MT, typename XT, typename YT>
-void launch_q4_k(const void* x, int M, int K, const Q4Batch& batch, size_t lds,
-                 hipStream_t stream) {
-  const int nwg = (batch.total_rows + NW * R - 1) / (NW * R);
-  dim3 grid(nwg, (M + MT - 1) / MT);
-  const int items = MT * (K / 32), threads = NW * 64;
-  if (sizeof(XT) == 2 && items <= threads)
-    hipLaunchKernelGGL((q4_gemv_kernel<NW, R, U, MT, 1, XT, YT>), grid, dim3(threads), lds, stream,
-                       reinterpret_cast<const XT*>(x), M, K, batch);
-  else if (sizeof(XT) == 2 && items <= 2 * threads)
-    hipLaunchKernelGGL((q4_gemv_kernel<NW, R, U, MT, 2, XT, YT>), grid, dim3(threads), lds, stream,
-                       reinterpret_cast<const XT*>(x), M, K, batch);
-  else
-    hipLaunchKernelGGL((q4_gemv_kernel<NW, R, U, MT, 0, XT, YT>), grid, dim3(threads), lds, stream,
-                       reinterpret_cast<const XT*>(x), M, K, batch);
-}
-
-template <int NW, int R, int MT, typename XT, typename YT>
-bool launch_q4_u(const GemvShape& g, const void* x, int M, int K, const Q4Batch& batch,
-                 size_t lds, hipStream_t s) {
-  switch (g.u) {
-    case 2: launch_q4_k<NW, R, 2, MT, XT, YT>(x, M, K, batch, lds, s); return true;
-    case 4: launch_q4_k<NW, R, 4, MT, XT, YT>(x, M, K, batch, lds, s); return true;
-    case 7: launch_q4_k<NW, R, 7, MT, XT, YT>(x, M, K, batch, lds, s); return true;
-    case 8: launch_q4_k<NW, R, 8, MT, XT, YT>(x, M, K, batch, lds, s); return true;
-  }
-  return false;
-}
-
-template <typename XT, typename YT>
-int dispatch_q4(strata_ctx* ctx, const void* x, int M, int K, const Q4Batch& batch,
-                hipStream_t stream) {
-  const int nv = K / 32;
-  GemvShape g = pick_shape(nv, batch.total_rows, M);
-  const size_t per_row = (size_t)nv * ((sizeof(XT) == 2 ? 64 : 128) + 4);
-  while (g.mt > 1 && g.mt * per_row > (size_t)ctx->max_lds_per_block) g.mt /= 2;
-  const size_t lds = g.mt * per_row;
-  STRATA_REQUIRE((int64_t)lds <= ctx->max_lds_per_block,
-                 "q4 GEMV: K=%d needs %zu B of LDS, device allows %d", K, lds,
-                 ctx->max_lds_per_block);
-  bool ok = false;
-  if constexpr (sizeof(XT) == 4) {
-    // fp32 activations (reference dtype flow): one geometry
-    g.u = 4;
-    if (g.mt == 4) ok = launch_q4_u<4, 2, 4, XT, YT>(g, x, M, K, batch, lds, stream);
-    else if (g.mt == 2) ok = launch_q4_u<4, 2, 2, XT, YT>(g, x, M, K, batch, lds, stream);
-    else ok = launch_q4_u<4, 2, 1, XT, YT>(g, x, M, K, batch, lds, stream);
-  } else {
-    if (g.mt == 4) ok = launch_q4_u<4, 2, 4, XT, YT>(g, x, M, K, batch, lds, stream);
-    else if (g.mt == 2) ok = launch_q4_u<4, 2, 2, XT, YT>(g, x, M, K, batch, lds, stream);
-    else if (g.nw == 4 && g.r == 4) ok = launch_q4_u<4, 4, 1, XT, YT>(g, x, M, K, batch, lds, stream);
-    else if (g.nw == 4 && g.r == 2) ok = launch_q4_u<4, 2, 1, XT, YT>(g, x, M, K, batch, lds, stream);
-    else if (g.nw == 4 && g.r == 1) ok = launch_q4_u<4, 1, 1, XT, YT>(g, x, M, K, batch, lds, stream);
-    else if (g.nw == 8 && g.r == 1) ok = launch_q4_u<8, 1, 1, XT, YT>(g, x, M, K, batch, lds, stream);
-    else if (g.nw == 8 && g.r == 2) ok = launch_q4_u<8, 2, 1, XT, YT>(g, x, M, K, batch, lds, stream);
-    else if (g.nw == 16 && g.r == 1) ok = launch_q4_u<16, 1, 1, XT, YT>(g, x, M, K, batch, lds, stream);
-  }
-  if (!ok)
-    return strata_set_error(STRATA_EINVAL, "q4 GEMV: no kernel for geometry nw=%d r=%d u=%d mt=%d",
-                            g.nw, g.r, g.u, g.mt);
-  STRATA_HIP_CHECK(hipGetLastError());
-  return STRATA_OK;
-}
-
-}  // namespace
-
-int strata_q4_gemv_epi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
-                       int count, const GemvEpilogue& e, void* stream) {
-  STRATA_REQUIRE(e.mode == EPI_SILU_PAIR || e.mode == EPI_ROPE_KV, "unknown GEMV epilogue");
-  Q4Batch batch{};
-  batch.count = count;
-  batch.epi = e.mode;
-  int rows = 0;
-  for (int i = 0; i < count; ++i) {
-    batch.p[i].w = reinterpret_cast<const uint4*>(ws[i].w);
-    batch.p[i].s = ws[i].scales;
-    batch.p[i].b = ws[i].biases;
-    batch.p[i].y = ws[i].y;
-    batch.p[i].n = static_cast<int>(ws[i].N);
-    batch.p[i].row0 = rows;
-    rows += static_cast<int>(ws[i].N);
-  }
-  batch.total_rows = rows;
-  if (e.mode == EPI_SILU_PAIR)
-    STRATA_REQUIRE(count == 2 && ws[0].N == ws[1].N, "SiLU pair epilogue needs gate/up of one size");
-  if (e.mode == EPI_ROPE_KV) {
-    STRATA_REQUIRE(count == 3 && e.head_dim % 2 == 0 &&
-                       ws[0].N == (int64_t)e.n_heads * e.head_dim &&
-                       ws[1].N == (int64_t)e.n_kv_heads * e.head_dim && ws[2].N == ws[1].N,
-                   "RoPE/KV epilogue needs q/k/v of [Hq*D, Hkv*D, Hkv*D] rows");
-    batch.head_dim = e.head_dim;
-    batch.n_heads = e.n_heads;
-    batch.n_kv_heads = e.n_kv_heads;
-    batch.lmax = e.lmax;
-    batch.pos0 = e.pos0;
-    batch.dpos = e.dpos;
-    batch.theta = e.theta;
-    batch.q_out = e.q_out;
-    batch.kc = e.kc;
-    batch.vc = e.vc;
-  }
-  // both epilogues need a wave to own a row pair: R = 2 with even row blocks
-  const int nv = K / 32;
-  const int MT = M >= 4 ? 4 : (M >= 2 ? 2 : 1);
-  STRATA_REQUIRE(M <= 8 && (size_t)MT * nv * 68 <= (size_t)ctx->max_lds_per_block &&
-                     MT * nv <= 2 * 4 * 64 && nv <= 64 * 8,
-                 "GEMV epilogue: unsupported shape M=%d K=%d", M, K);
-  const int u = nv <= 128 ? 2 : (nv <= 256 ? 4 : (nv <= 448 ? 7 : 8));
-  const size_t lds = (size_t)MT * nv * 68;
-  GemvShape g{4, 2, u, MT};
-  hipStream_t s = as_stream(stream);
-  bool ok;
-  if (MT == 4) ok = launch_q4_u<4, 2, 4, bf16_t, bf16_t>(g, x, M, K, batch, lds, s);
-  else if (MT == 2) ok = launch_q4_u<4, 2, 2, bf16_t, bf16_t>(g, x, M, K, batch, lds, s);
-  else ok = launch_q4_u<4, 2, 1, bf16_t, bf16_t>(g, x, M, K, batch, lds, s);
-  if (!ok) return strata_set_error(STRATA_EINVAL, "GEMV epilogue: no kernel for K=%d", K);
-  STRATA_HIP_CHECK(hipGetLastError());
-  return STRATA_OK;
-}
+// Entry points of the decode-side q4 GEMV and the bf16 GEMV (lm_head); the
+// kernels and their design notes are in q4_gemv_impl.h.
+#include "q4_gemv_impl.h"
 
 int strata_q4_gemv(strata_ctx* ctx, const void* x, int x_dtype, int M, int K,
                    const strata_q4_weight* ws, int count, int y_dtype, void* stream) {
-  Q4Batch batch{};
-  batch.count = count;
-  int rows = 0;
-  for (int i = 0; i < count; ++i) {
-    batch.p[i].w = reinterpret_cast<const uint4*>(ws[i].w);
-    batch.p[i].s = ws[i].scales;
-    batch.p[i].b = ws[i].biases;
-    batch.p[i].y = ws[i].y;
-    batch.p[i].n = static_cast<int>(ws[i].N);
-    batch.p[i].row0 = rows;
-    rows += static_cast<int>(ws[i].N);
-  }
-  batch.total_rows = rows;
+  Q4Batch batch = make_batch(ws, count, EPI_STORE);
   hipStream_t s = as_stream(stream);
+  const NormArgs na{nullptr, 0.f};
   if (x_dtype == STRATA_BF16 && y_dtype == STRATA_BF16)
-    return dispatch_q4<bf16_t, bf16_t>(ctx, x, M, K, batch, s);
+    return dispatch_q4<EPI_STORE, false, bf16_t, bf16_t>(ctx, x, M, K, batch, na, s);
   if (x_dtype == STRATA_BF16 && y_dtype == STRATA_F32)
-    return dispatch_q4<bf16_t, float>(ctx, x, M, K, batch, s);
+    return dispatch_q4<EPI_STORE, false, bf16_t, float>(ctx, x, M, K, batch, na, s);
   if (x_dtype == STRATA_F32 && y_dtype == STRATA_F32)
-    return dispatch_q4<float, float>(ctx, x, M, K, batch, s);
+    return dispatch_q4<EPI_STORE, false, float, float>(ctx, x, M, K, batch, na, s);
   if (x_dtype == STRATA_F32 && y_dtype == STRATA_BF16)
-    return dispatch_q4<float, bf16_t>(ctx, x, M, K, batch, s);
+    return dispatch_q4<EPI_STORE, false, float, bf16_t>(ctx, x, M, K, batch, na, s);
   return strata_set_error(STRATA_EINVAL, "q4 GEMV: unsupported dtype pair (%d, %d)", x_dtype,
                           y_dtype);
 }

@@ -140,6 +140,8 @@ struct AttnExtra {
   float* part = nullptr;      // caller-owned split-K partials [B, Hq, splits, D + 2]
   int part_splits = 0;        // splits the partials buffer holds
   int out_tm = 0;             // prefill: write token-major [B, Lq, Hq, D]
+  int* arrive = nullptr;      // decode: zeroed per-(b, kv head) arrival counters [B * Hkv];
+                              // the last split-K workgroup merges in-kernel
 };
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

@@ -10,8 +10,10 @@ inline bool dtype_ok(int d) { return d == STRATA_F32 || d == STRATA_BF16; }
 inline size_t dtype_size(int d) { return d == STRATA_F32 ? 4 : 2; }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// GEMV epilogues used by the decode engine (mode 1: SiLU pair of gate/up,
-// mode 2: RoPE + KV append of q/k/v); bf16 x, M <= 8.
+// GEMV prologue/epilogues used by the decode engine (bf16 x, M <= 8).
+// mode 0: plain store; 1: SiLU pair of gate/up; 2: RoPE + KV append of
+// q/k/v; 3: residual add in place (y is the residual stream).  norm_w != null
+// applies RMSNorm (weight norm_w, eps) to x first.
 struct GemvEpilogue {
   int mode;
   int head_dim, n_heads, n_kv_heads, lmax, pos0;
@@ -20,9 +22,13 @@ struct GemvEpilogue {
   uint16_t* q_out;
   uint16_t* kc;
   uint16_t* vc;
+  const uint16_t* norm_w;
+  float eps;
 };
 int strata_q4_gemv_epi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
                        int count, const GemvEpilogue& e, void* stream);
+int strata_q4_gemv_resid(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
+                         int count, void* stream);
 int strata_q4_gemv(strata_ctx* ctx, const void* x, int x_dtype, int M, int K,
                    const strata_q4_weight* ws, int count, int y_dtype, void* stream);
 int strata_bf16_gemv(strata_ctx* ctx, const void* x, int M, int K, const uint16_t* w, int N,
