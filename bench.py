@@ -1,17 +1,32 @@
 """Benchmark: Llama-3-8B-shaped q4 decode at batch 1 on one MI355X.
 
-One "step" = one greedy decode token through the full 32-layer 8B-shaped
-model (q4 group-64 linears, bf16 embedding / lm_head, bf16 KV cache, RoPE
-theta 5e5) after a 2048-token prefill, with every input already resident in
-HBM.  ``value`` is decode tokens/s.
+Headline (``value``): one "step" = one greedy decode token through the full
+32-layer 8B-shaped model (q4 group-64 linears, bf16 embedding / lm_head, bf16
+KV cache, RoPE theta 5e5) after a 2048-token prefill, with every input already
+resident in HBM; ``value`` is decode tokens/s, the decode step replayed as a
+HIP graph by the native engine.
 
-The same run measures the dominant kernel, the q4 GEMV, on the BASELINE
-config-2 six-linear set ([4096->4096], [4096->1024] x2, [4096->14336] x2,
-[14336->4096]) as the decode driver launches it (q/k/v in one launch,
-gate/up in one launch, down alone), timing every launch with HIP events on
-the stream it runs on -> ``roofline``; and times the CPU restatement
-(oracle/libstrata_oracle.so, OpenMP on all host cores) on a bounded sample
-of the same per-token work -> ``cpu_baseline``.
+``roofline``: the dominant kernel, the q4 GEMV, on the six-linear set of
+config 2 ([4096->4096], [4096->1024] x2, [4096->14336] x2, [14336->4096]) as
+the decode engine launches it (q/k/v in one launch, gate/up in one launch,
+down alone).  Each launch kind is captured ``--gemv-iters`` times back to
+back into one graph; HIP events on the capture stream bracket its replay, so
+the average launch duration excludes host launch cost (it is the figure the
+kernel-trace profile reports).  Weights rotate through six copies (680 MB) so
+no launch finds them in the 256 MB Infinity Cache.
+
+Further measurements on the same line (the other configs of the workload):
+``attention_decode`` (config 3: cached decode GQA over bf16 KV, GB/s),
+``prefill`` (config 5: q4 GEMM at M=8192 on MFMA and causal GQA prefill
+attention, TFLOP/s), ``e2e_3b`` (config 4: Llama-3.2-3B-shaped greedy
+generation, 2048-token prompt + 256 tokens), ``config1`` (fp32 chunked GQA +
+RoPE latency) and ``cpu_baseline`` (the C restatement of the oracle on the
+host cores, on a bounded sample of the per-token work).
+
+``--profile gemv`` runs only the GEMV launches plus a 256 MiB device copy (a
+plain copy kernel of known size), for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+passes; the measured HBM bytes per launch are kept in
+profiles/q4_gemv_traffic.json and reported as ``roofline.traffic``.
 """
 from __future__ import annotations
 
@@ -27,6 +42,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 PROMPT = 2048
 
 
@@ -37,7 +53,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=8)
     p.add_argument("--prompt", type=int, default=PROMPT)
     p.add_argument("--gemv-iters", type=int, default=50)
-    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
+    p.add_argument("--profile", choices=["gemv"], default=None)
     return p.parse_args()
 
 
@@ -45,8 +63,34 @@ def q4_bytes(n, k, m=1):
     return n * k // 2 + 2 * 2 * n * (k // 64) + 2 * k * m + 2 * n * m
 
 
-def gemv_roofline(iters):
-    """Time the decode-layer q4 GEMV launches with HIP events on their stream."""
+def graph_time_us(fn, iters, warm=2):
+    """Average duration of `fn` captured `iters` times into one HIP graph,
+    timed with events on the capture stream."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(warm):
+            fn(0)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(iters):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    g.replay()
+    b.record(st)
+    torch.cuda.synchronize()
+    del g
+    return 1e3 * a.elapsed_time(b) / iters
+
+
+def gemv_sets():
     import torch
     from lokahi_amd import ops
     dev = torch.device("cuda", 0)
@@ -55,8 +99,6 @@ def gemv_roofline(iters):
     def q4(n, k):
         return ops.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02)
 
-    # Six copies of the six-linear set (680 MB) are cycled so that no launch
-    # finds its weights in the 256 MB last-level (Infinity) cache.
     copies = 6
     sets = [{"q": q4(4096, 4096), "k": q4(1024, 4096), "v": q4(1024, 4096),
              "gate": q4(14336, 4096), "up": q4(14336, 4096), "down": q4(4096, 14336)}
@@ -75,38 +117,179 @@ def gemv_roofline(iters):
         ("down", lambda W: ops.linear_multi(xd, [W["down"]], outs=[outs["down"]]),
          q4_bytes(4096, 14336)),
     ]
-    stream = torch.cuda.current_stream(dev)
-    for _, fn, _ in launches:
-        for c in range(copies):
-            fn(sets[c])
-    torch.cuda.synchronize()
+    return sets, launches
+
+
+def gemv_roofline(iters):
+    sets, launches = gemv_sets()
+    copies = len(sets)
     per = {}
     for name, fn, nbytes in launches:
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(iters)]
-        # A spin kernel holds the stream while the host enqueues every timed
-        # launch, so the event pairs bracket back-to-back kernels, not host
-        # launch latency.
-        torch.cuda._sleep(200_000_000)
-        for it, (a, b) in enumerate(evs):
-            a.record(stream)
-            fn(sets[it % copies])
-            b.record(stream)
-        torch.cuda.synchronize()
-        ms = sorted(a.elapsed_time(b) for a, b in evs)
-        per[name] = {"bytes": nbytes, "avg_us": 1e3 * sum(ms) / len(ms),
-                     "median_us": 1e3 * ms[len(ms) // 2]}
+        us = graph_time_us(lambda i, fn=fn: fn(sets[i % copies]), iters)
+        per[name] = {"bytes": nbytes, "avg_us": round(us, 3), "GBps": round(nbytes / (us * 1e3), 1)}
     tot_bytes = sum(v["bytes"] for v in per.values())
     tot_us = sum(v["avg_us"] for v in per.values())
-    for v in per.values():
-        v["GBps"] = v["bytes"] / (v["avg_us"] * 1e3)
     achieved = tot_bytes / (tot_us * 1e3)
+    traffic = None
+    tf = ROOT / "profiles" / "q4_gemv_traffic.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_set")
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "kernel": "q4_gemv_kernel (six-linear set, 3 launches)",
-            "bytes_per_set": tot_bytes, "us_per_set": round(tot_us, 2),
-            "launches": {k: {kk: round(vv, 3) if isinstance(vv, float) else vv
-                             for kk, vv in v.items()} for k, v in per.items()}}
+            "bytes_per_set": tot_bytes, "us_per_set": round(tot_us, 2), "launches": per}
+
+
+def profile_gemv(iters):
+    """Only the GEMV launches plus a 256 MiB copy (for rocprofv3 --pmc passes)."""
+    import torch
+    sets, launches = gemv_sets()
+    for name, fn, _ in launches:
+        for i in range(iters):
+            fn(sets[i % len(sets)])
+    a = torch.empty(64 * 2**20, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": "gemv", "iters": iters, "copy_bytes_read": a.numel() * 4}))
+
+
+def attention_decode():
+    """Config 3: Hq32/Hkv8, D128, bf16 KV; append one token, then attend."""
+    import torch
+    from lokahi_amd import ops
+    dev = torch.device("cuda", 0)
+    res = []
+    for B, L in [(1, 1024), (1, 8192), (1, 32768), (16, 1024), (16, 8192), (16, 32768)]:
+        g = torch.Generator(device=dev).manual_seed(B * 7 + L)
+        q = torch.randn((B, 32, 1, 128), generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn((B, 8, L + 1, 128), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((B, 8, L + 1, 128), generator=g, device=dev).to(torch.bfloat16)
+        us = graph_time_us(lambda i: ops.attention(q, k, v), 10)
+        kv = B * 8 * (L + 1) * 128 * 2 * 2
+        res.append({"batch": B, "context": L, "us": round(us, 2), "kv_bytes": kv,
+                    "GBps": round(kv / (us * 1e3), 1),
+                    "frac_hbm": round(kv / (us * 1e3) / HBM_PEAK_GBS, 4)})
+        del q, k, v
+    torch.cuda.empty_cache()
+    return res
+
+
+def prefill_8b():
+    """Config 5: q4 GEMM at M=8192 over the seven 8B linears + causal GQA prefill."""
+    import torch
+    from lokahi_amd import ops
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(5)
+    M = 8192
+    shapes = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+              ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+    x = torch.randn((M, 4096), generator=g, device=dev).to(torch.bfloat16)
+    xd = torch.randn((M, 14336), generator=g, device=dev).to(torch.bfloat16)
+    tot_us, flops = 0.0, 0
+    per = {}
+    for name, n, k in shapes:
+        w = ops.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02)
+        xi = xd if k == 14336 else x
+        us = graph_time_us(lambda i: ops.linear(xi, *w), 3, warm=1)
+        f = 2 * M * n * k
+        per[name] = {"us": round(us, 1), "TFLOPs": round(f / us / 1e6, 1)}
+        tot_us += us
+        flops += f
+        del w
+    gemm = flops / tot_us / 1e6
+    q = torch.randn((1, 32, M, 128), generator=g, device=dev).to(torch.bfloat16)
+    kk = torch.randn((1, 8, M, 128), generator=g, device=dev).to(torch.bfloat16)
+    vv = torch.randn((1, 8, M, 128), generator=g, device=dev).to(torch.bfloat16)
+    aus = graph_time_us(lambda i: ops.attention(q, kk, vv, q_block_size=512, k_block_size=512),
+                        3, warm=1)
+    aflops = 4 * 32 * 128 * (M * (M + 1) // 2)
+    del q, kk, vv, x, xd
+    torch.cuda.empty_cache()
+    return {"tokens": M,
+            "q4_gemm": {"us_per_layer": round(tot_us, 1), "TFLOPs": round(gemm, 1),
+                        "frac_mfma_bf16": round(gemm / MFMA_BF16_PEAK_TFLOPS, 4),
+                        "linears": per},
+            "attention": {"us": round(aus, 1), "TFLOPs": round(aflops / aus / 1e6, 1),
+                          "frac_mfma_bf16": round(aflops / aus / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}}
+
+
+def run_decode(cfg, prompt_len, new_tokens, seed):
+    """Prefill `prompt_len` uniform-random ids, then time `new_tokens` greedy
+    tokens on the native engine (warm pass first, so the step graphs exist)."""
+    import torch
+    from lokahi_amd.llama import DecoderEngine, HipLlamaForCausalLM, random_weights
+    weights = random_weights(cfg, seed=seed)
+    model = HipLlamaForCausalLM(cfg, weights)
+    cache = model.new_cache(1, prompt_len + new_tokens + 8)
+    engine = DecoderEngine(model, cache, max_batch=1, max_tokens=prompt_len)
+    gen = torch.Generator().manual_seed(seed)
+    prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=gen)
+    times = []
+    for rep in range(2):  # rep 0 warms up (captures the per-bucket step graphs)
+        cache.clear()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        engine.forward(prompt[:, :-1])
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        toks = engine.generate(prompt[:, -1:], new_tokens)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        times.append((t1 - t0, t2 - t1))
+    prefill_s, decode_s = times[-1]
+    del engine, model, weights, cache
+    torch.cuda.empty_cache()
+    return prefill_s, decode_s, toks
+
+
+def decode_bytes(cfg, ctx_avg):
+    lin = (cfg.hidden_size * cfg.hidden_size * 2  # q, o
+           + 2 * cfg.hidden_size * cfg.num_key_value_heads * cfg.head_dim  # k, v
+           + 3 * cfg.hidden_size * cfg.intermediate_size)  # gate, up, down
+    q4 = lin // 2 + 4 * (lin // 64)
+    kv = 2 * 2 * cfg.num_key_value_heads * cfg.head_dim * ctx_avg
+    return cfg.num_hidden_layers * (q4 + kv) + cfg.vocab_size * cfg.hidden_size * 2
+
+
+def e2e_3b():
+    """Config 4: Llama-3.2-3B-shaped greedy generation, 2048-token prompt + 256 tokens."""
+    from lokahi_amd.llama import LLAMA32_3B
+    n = 256
+    prefill_s, decode_s, _ = run_decode(LLAMA32_3B, 2048, n, seed=77)
+    tok_s = n / decode_s
+    byts = decode_bytes(LLAMA32_3B, 2048 + n // 2)
+    return {"model": "Llama-3.2-3B shape (28 layers, 3072/8192, 24q/8kv heads, vocab 128256)",
+            "prompt": 2048, "new_tokens": n, "decode_tok_s": round(tok_s, 1),
+            "prefill_s": round(prefill_s, 4), "bytes_per_token": byts,
+            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / byts, 1),
+            "frac_of_roofline": round(tok_s * byts / (HBM_PEAK_GBS * 1e9), 4)}
+
+
+def config1():
+    """Config 1: B1, Hq8/Hkv2, D64, L512, chunks 128, RoPE theta 1e4, fp32."""
+    import torch
+    from lokahi_amd import ops
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(1)
+    q = torch.randn((1, 8, 513, 64), generator=g, device=dev)
+    k = torch.randn((1, 2, 513, 64), generator=g, device=dev)
+    v = torch.randn((1, 2, 513, 64), generator=g, device=dev)
+    pos = torch.arange(513, device=dev, dtype=torch.int32)[None]
+    qp, kp, vp, posp = q[:, :, :512].contiguous(), k[:, :, :512].contiguous(), \
+        v[:, :, :512].contiguous(), pos[:, :512].contiguous()
+    qd = q[:, :, 512:].contiguous()
+    posd = torch.tensor([[512]], dtype=torch.int32, device=dev)
+
+    def pre(i):
+        ops.rope(qp, kp, posp, 10000.0)
+        ops.attention(qp, kp, vp, query_positions=posp, q_block_size=128, k_block_size=128)
+
+    def dec(i):
+        ops.attention(qd, k, v, query_positions=posd)
+    return {"prefill_us": round(graph_time_us(pre, 20), 2),
+            "decode_us": round(graph_time_us(dec, 20), 2)}
 
 
 def cpu_baseline(prompt):
@@ -170,45 +353,23 @@ def cpu_baseline(prompt):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+        print(json.dumps({"error": "this build measures one GPU only (no multi-GPU path); "
+                                   "run with --gpus 1"}))
         sys.exit(2)
     import torch
-    from lokahi_amd.llama import LLAMA3_8B, DecoderEngine, HipLlamaForCausalLM, random_weights
-    from lokahi_amd import ops
+    if args.profile == "gemv":
+        profile_gemv(args.gemv_iters)
+        return
+    from lokahi_amd.llama import LLAMA3_8B
 
     cfg = LLAMA3_8B
-    torch.manual_seed(0)
-    weights = random_weights(cfg, seed=1234)
-    model = HipLlamaForCausalLM(cfg, weights)
-    K = args.steps + 1  # tokens per timed generate call (first one is host-launched)
-    cache = model.new_cache(1, args.prompt + 2 * K + 8)
-    engine = DecoderEngine(model, cache, max_batch=1, max_tokens=args.prompt)
-    gen = torch.Generator().manual_seed(0)
-    prompt = torch.randint(0, cfg.vocab_size, (1, args.prompt), generator=gen)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    logits = engine.forward(prompt[:, :-1])  # prefill prompt[:-1]
-    torch.cuda.synchronize()
-    prefill_s = time.perf_counter() - t0
-    # warmup: one full generate call of K tokens (captures the decode-step
-    # HIP graph, which the timed call replays)
-    toks = engine.generate(prompt[:, -1:], K)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    toks = engine.generate(toks[:, -1:], K)  # K greedy decode steps, graph-replayed
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = 1e3 * elapsed / K
-    tok_s = K / elapsed
-    del logits
+    K = args.steps + 1  # tokens per timed generate call
+    prefill_s, decode_s, _ = run_decode(cfg, args.prompt, K, seed=1234)
+    tok_s = K / decode_s
+    ms_per_step = 1e3 * decode_s / K
+    token_bytes = decode_bytes(cfg, args.prompt + K // 2)
 
     roof = gemv_roofline(args.gemv_iters)
-    # bytes one decode token must stream at this context (weights + KV + lm_head)
-    lin = sum(q4_bytes(n, k) for n, k in [(4096, 4096), (1024, 4096), (1024, 4096),
-                                          (4096, 4096), (14336, 4096), (14336, 4096),
-                                          (4096, 14336)])
-    ctx = args.prompt + K + K // 2
-    token_bytes = cfg.num_hidden_layers * (lin + 2 * 2 * 8 * 128 * ctx) + cfg.vocab_size * 4096 * 2
     line = {
         "metric": "decode tok/s, Llama-3-8B-shape q4 bs=1; q4 GEMV HBM GB/s (% of peak)",
         "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": K,
@@ -226,6 +387,11 @@ def main():
         "prefill_s": round(prefill_s, 3),
         "roofline": roof,
     }
+    if not args.no_extra:
+        line["attention_decode"] = attention_decode()
+        line["prefill"] = prefill_8b()
+        line["e2e_3b"] = e2e_3b()
+        line["config1"] = config1()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.prompt)
     print(json.dumps(line), flush=True)

@@ -177,6 +177,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     for (int jj = 0; jj < J; ++jj) {
       kr[jj].to_float(kx[jj]);
       vr[jj].to_float(vx[jj]);
+      // Keys past the count were fetched speculatively (any bits, NaN
+      // included): their weight is 0, and 0 * NaN must not reach o.
+      if (base + jj * 4 * KPW + sub >= t1) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) vx[jj][e] = 0.f;
+      }
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -222,7 +228,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   // (wave, sub) publishes its (m, s, o[D]) per head, then all threads
   // combine them, GB heads per round.
   constexpr int NS = 4 * KPW;
-  constexpr int GB = G < 4 ? G : 4;
+  constexpr int GB = G <= 4 ? G : (G % 4 == 0 ? 4 : G / 2);  // heads per LDS round
+  static_assert(G % GB == 0, "head rounds must tile the group");
   __shared__ float sm_m[NS][GB], sm_s[NS][GB];
   __shared__ float sm_o[NS][GB][D];
   const int stream = wave * KPW + sub;
@@ -671,8 +678,10 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
     hipLaunchKernelGGL((attn_decode_kernel<TQ, TK, TV, D, GV>), grid, dim3(256), 0, stream,   \
                        (const TQ*)q, (const TK*)k, (const TV*)v, kv_bs, kv_hs, qpos, Hq, Hkv, \
                        Lk, ex.dlen, causal, chunk, nsplit, scale, eps, part, arrive, (TQ*)out);
-  STRATA_DEC(1) else STRATA_DEC(2) else STRATA_DEC(4) else STRATA_DEC(8) else
-    return strata_set_error(STRATA_ENOTSUP, "decode attention: group size %d not in {1,2,4,8}", G);
+  STRATA_DEC(1) else STRATA_DEC(2) else STRATA_DEC(3) else STRATA_DEC(4) else STRATA_DEC(6) else
+  STRATA_DEC(8) else
+    return strata_set_error(STRATA_ENOTSUP, "decode attention: group size %d not in {1,2,3,4,6,8}",
+                            G);
 #undef STRATA_DEC
   STRATA_HIP_CHECK(hipGetLastError());
   if (nsplit > 1 && arrive == nullptr) {
@@ -700,7 +709,7 @@ int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v,
                    int D, int causal, float scale, float eps, void* out, const AttnExtra& ex,
                    hipStream_t stream) {
   const int G = Hq / Hkv;
-  const bool g_ok = G == 1 || G == 2 || G == 4 || G == 8;
+  const bool g_ok = G == 1 || G == 2 || G == 3 || G == 4 || G == 6 || G == 8;
   if (Lq == 1 && g_ok && (D == 64 || D == 128)) {
     if (D == 64)
       return launch_decode<TQ, TK, TV, 64>(ctx, q, k, v, kv_bs, kv_hs, qpos, B, Hq, Hkv, Lk,

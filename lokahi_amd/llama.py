@@ -245,6 +245,7 @@ class DecoderEngine:
         self.handle = h
         self._layers = layers  # keep the struct array alive with the handle
         self.vocab = cfg.vocab_size
+        self._outs = {}
 
     def forward(self, ids: torch.Tensor) -> torch.Tensor:
         """Last-position fp32 logits [B, vocab] for ids [B, L] appended to the cache."""
@@ -265,7 +266,13 @@ class DecoderEngine:
         from .ops import _stream
         ids32 = prompt.to(device=self.model.device, dtype=torch.int32).contiguous()
         B, L = ids32.shape
-        out = torch.empty((B, max_new), dtype=torch.int32, device=self.model.device)
+        # one output buffer per (B, max_new): the native engine reuses its
+        # captured decode-step graphs only while the output address is stable
+        key = (B, max_new)
+        if key not in self._outs:
+            self._outs[key] = torch.empty((B, max_new), dtype=torch.int32,
+                                          device=self.model.device)
+        out = self._outs[key]
         _abi.check(self._lib.strata_decoder_generate(
             self.handle, ids32.data_ptr(), B, L, max_new, float(temperature),
             1 if use_graph else 0, out.data_ptr(), _stream(self.model.device.index or 0)))

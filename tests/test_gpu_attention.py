@@ -168,3 +168,22 @@ def test_decode_equals_last_row_of_prefill_and_chunk_independence(dev):
     np.testing.assert_allclose(full[:, :, -1:], last, atol=1e-4, rtol=1e-4)
     other = ops.attention(_t(q, dev), _t(k, dev), _t(v, dev), q_block_size=7, k_block_size=3)
     np.testing.assert_allclose(full, other.cpu().numpy(), atol=1e-6)
+
+
+@pytest.mark.parametrize("Hq,dtype", [(24, "bf16"), (48, "bf16"), (24, "f32")])
+def test_decode_group_sizes_3_and_6(dev, Hq, dtype):
+    """GQA groups of 3 (Llama-3.2-3B: 24 query / 8 KV heads) and 6 on the split-K decode kernel."""
+    from lokahi_amd import ops
+    rng = np.random.default_rng(Hq)
+    B, Hkv, D, L = 2, 8, 128, 700
+    q = round_bf16(rng.normal(size=(B, Hq, 1, D)).astype(np.float32))
+    k = round_bf16(rng.normal(size=(B, Hkv, L, D)).astype(np.float32))
+    v = round_bf16(rng.normal(size=(B, Hkv, L, D)).astype(np.float32))
+    if dtype == "bf16":
+        out = to_np_f32(ops.attention(bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev)))
+        tol = TOL_BF16
+    else:
+        out = ops.attention(_t(q, dev), _t(k, dev), _t(v, dev)).cpu().numpy()
+        tol = TOL_F32
+    ref = att.chunked_gqa(q, k, v, None, True, 32768, 1024)
+    assert rel_err(out, ref) < tol

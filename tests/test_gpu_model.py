@@ -109,3 +109,37 @@ def test_engine_rejects_capacity_overflow(dev):
     e = DecoderEngine(model, cache, max_batch=1, max_tokens=8)
     with pytest.raises(ValueError, match="capacity"):
         e.generate(torch.zeros((1, 6), dtype=torch.int64), 4)
+
+
+GQA3 = oll.Config(vocab_size=300, hidden_size=384, intermediate_size=512, num_hidden_layers=2,
+                  num_attention_heads=6, num_key_value_heads=2, rms_norm_eps=1e-5,
+                  rope_theta=500000.0)
+
+
+def test_engine_group3_across_key_bucket(dev):
+    """Llama-3.2-3B head grouping (G = 3) on the graph-replayed engine; the decode
+    steps cross a 256-key capacity bucket, so two captured step graphs serve them.
+    Seed 46: the oracle's top-2 logit margin is >= 0.087 at every step (a seed
+    whose margin is ~0.006 at one step flips that argmax under bf16 rounding)."""
+    model, ref = _pair(GQA3, seed=46, std=0.05)
+    prompt = np.random.default_rng(46).integers(0, GQA3.vocab_size, (1, 250))
+    got = model.generate(torch.from_numpy(prompt), max_new_tokens=12).cpu().numpy()
+    exp = oll.greedy_generate(ref, prompt, max_new_tokens=12, cache=OracleKVCache(2))
+    assert np.array_equal(got, exp), f"\n{got[:, 250:]}\n{exp[:, 250:]}"
+
+
+def test_engine_ignores_unwritten_cache_slots(dev):
+    """Cache slots past the current length hold arbitrary bits (here NaN): the
+    graph-mode decode attention may fetch them ahead of the key count, but they
+    must not reach the output (regression test).  Seed 54: top-2 logit margin
+    >= 0.066 at every step."""
+    from lokahi_amd.llama import DecoderEngine
+    model, ref = _pair(GQA3, seed=54, std=0.05)
+    cache = model.new_cache(1, 320)
+    cache.k_storage.fill_(float("nan"))
+    cache.v_storage.fill_(float("nan"))
+    eng = DecoderEngine(model, cache, max_batch=1, max_tokens=256)
+    prompt = np.random.default_rng(54).integers(0, GQA3.vocab_size, (1, 61))
+    got = eng.generate(torch.from_numpy(prompt), 10).cpu().numpy()
+    exp = oll.greedy_generate(ref, prompt, max_new_tokens=10, cache=OracleKVCache(2))
+    assert np.array_equal(got, exp), f"\n{got[:, 61:]}\n{exp[:, 61:]}"
