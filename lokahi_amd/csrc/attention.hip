@@ -406,7 +406,10 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
   constexpr bool kBF16 = sizeof(T) == 2;
   constexpr int KT = 64;                         // keys per tile
   constexpr int KPAD = kBF16 ? 8 : 4;            // LDS row padding (elements)
-  constexpr int VPAD = kBF16 ? 8 : 4;
+  // bf16 V is stored transposed [D][KT + VPAD]: a row of 68 elements is 34
+  // dwords, so one wave's transposed 2-byte writes (16 keys x 4 chunks, see
+  // tile_slot) land in 32 distinct banks, and 8-byte reads stay aligned.
+  constexpr int VPAD = 4;
   // K tile: [KT][D + KPAD]; V tile: bf16 -> transposed [D][KT + VPAD], f32 -> [KT][D + VPAD]
   constexpr int K_ELEMS = KT * (D + KPAD);
   constexpr int V_ELEMS = kBF16 ? D * (KT + VPAD) : KT * (D + VPAD);
@@ -457,17 +460,45 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
   float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = scale * kLog2e;
 
+  // K/V tiles are register-prefetched: tile t+1's global loads are issued
+  // right after tile t is written to LDS, so they are in flight during the
+  // tile's MFMAs and softmax.
+  constexpr int CH = 16 / sizeof(T);            // elements per 16-byte chunk
+  constexpr int NCH = KT * D / CH / 256;        // chunks per thread per tile
+  static_assert(KT * D / CH % 256 == 0, "tile chunks must divide over the block");
+  uint4 kreg[NCH], vreg[NCH];
+  // chunk c of the tile -> (key t, element d0): each wave covers 16 keys x 4
+  // consecutive 16-byte chunks (64-byte row segments).
+  auto tile_slot = [&](int c, int& t, int& d0) {
+    const int ln = c & 63, blk = c >> 6;
+    t = (blk & 3) * 16 + (ln & 15);
+    d0 = ((blk >> 2) * 4 + (ln >> 4)) * CH;
+  };
+  static_assert((D / CH) % 4 == 0, "tile_slot needs a multiple of 4 chunks per key");
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+      const int c = threadIdx.x + 256 * u;
+      int t, d0;
+      tile_slot(c, t, d0);
+      const int key = kb + t;
+      kreg[u] = make_uint4(0, 0, 0, 0);
+      vreg[u] = make_uint4(0, 0, 0, 0);
+      if (key < Lk) {
+        kreg[u] = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * D + d0);
+        vreg[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * D + d0);
+      }
+    }
+  };
+  if (kmax > 0) fetch(0);
   for (int kb0 = 0; kb0 < kmax; kb0 += KT) {
     // ---- stage K (row-major, padded) and V (bf16: transposed) tiles
-    constexpr int CH = 16 / sizeof(T);  // elements per 16-byte chunk
-    for (int c = threadIdx.x; c < KT * D / CH; c += 256) {
-      const int t = c / (D / CH), d0 = (c - t * (D / CH)) * CH;
-      const int key = kb0 + t;
-      uint4 ku = make_uint4(0, 0, 0, 0), vu = make_uint4(0, 0, 0, 0);
-      if (key < Lk) {
-        ku = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * D + d0);
-        vu = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * D + d0);
-      }
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+      const int c = threadIdx.x + 256 * u;
+      int t, d0;
+      tile_slot(c, t, d0);
+      const uint4 ku = kreg[u], vu = vreg[u];
       *reinterpret_cast<uint4*>(&ks[t * (D + KPAD) + d0]) = ku;
       if constexpr (kBF16) {
         const uint32_t uu[4] = {vu.x, vu.y, vu.z, vu.w};
@@ -482,6 +513,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
       }
     }
     __syncthreads();
+    if (kb0 + KT < kmax) fetch(kb0 + KT);
 
     // ---- S^T tiles: st[j][i] = score(query row, key kb0 + 16j + 4*grp + i)
     f32x4_t st[4];

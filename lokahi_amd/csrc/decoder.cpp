@@ -45,6 +45,7 @@ struct strata_decoder {
   int part_splits;
   int* arrive;            // split-K arrival counters [max_batch * num_kv_heads] (self-resetting)
   bool fused_merge;       // merge split-K partials in the attention kernel (else a merge launch)
+  float2* rope_table;     // (cos, sin) [Lmax][head_dim/2], built once at creation
   void* amax;             // argmax partials [max_batch * kArgmaxBlocks * 8 B]
   hipStream_t stream;     // the decoder's own stream (graph capture / replay)
   // Captured decode steps, one per key-capacity bucket: a step at key count
@@ -105,7 +106,7 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
       GemvEpilogue eq{2, D, Hq, Hkv, kv->Lmax, graph_mode ? 0 : pos0,
                       graph_mode ? d->counters + 1 : nullptr, c.rope_theta,
                       (uint16_t*)d->qr, (uint16_t*)kc, (uint16_t*)vc, Lw.input_norm,
-                      c.rms_norm_eps};
+                      c.rms_norm_eps, d->rope_table};
       RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, qkv, 3, eq, stream));
       AttnExtra ex;
       ex.part = d->part;
@@ -116,14 +117,15 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
                                    kv_bs, kv_hs, nullptr, B, Hq, Hkv, 1,
                                    graph_mode ? key_cap : pos0 + 1, D, 1, 1e-12f, d->attn, ex,
                                    stream));
-      GemvEpilogue er{3, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr, nullptr, 0.f};
+      GemvEpilogue er{3, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr, nullptr, 0.f,
+                      nullptr};
       strata_q4_weight o = Lw.o;
       o.y = d->h;
       RC(strata_q4_gemv_epi(d->ctx, d->attn, T, Hq * D, &o, 1, er, stream));
       strata_q4_weight gu[2] = {Lw.gate, Lw.up};
       gu[0].y = d->act;
       GemvEpilogue es{1, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr, Lw.post_norm,
-                      c.rms_norm_eps};
+                      c.rms_norm_eps, nullptr};
       RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, gu, 2, es, stream));
       strata_q4_weight dn = Lw.down;
       dn.y = d->h;
@@ -262,6 +264,7 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
       {reinterpret_cast<void**>(&d->counters), 16},
       {&d->amax, (size_t)max_batch * kArgmaxBlocks * 8},
       {reinterpret_cast<void**>(&d->arrive), (size_t)max_batch * c.num_kv_heads * 4},
+      {reinterpret_cast<void**>(&d->rope_table), (size_t)kv->Lmax * (c.head_dim / 2) * 8},
   };
   for (auto& b : bufs)
     if (!rc) rc = alloc(b.p, b.bytes);
@@ -269,6 +272,9 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
   if (!rc)
     rc = alloc(reinterpret_cast<void**>(&d->part),
                (size_t)kv->B * c.num_heads * d->part_splits * (c.head_dim + 2) * 4);
+  if (!rc) rc = strata_rope_table_launch(d->rope_table, kv->Lmax, c.head_dim, c.rope_theta, nullptr);
+  if (!rc && hipDeviceSynchronize() != hipSuccess)
+    rc = strata_set_error(STRATA_EHIP, "decoder: RoPE table initialisation failed");
   if (!rc && hipMemset(d->arrive, 0, (size_t)max_batch * c.num_kv_heads * 4) != hipSuccess)
     rc = strata_set_error(STRATA_EHIP, "decoder: counter initialisation failed");
   if (!rc && hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess)
@@ -286,7 +292,8 @@ int strata_decoder_destroy(strata_decoder* d) {
   hipDeviceSynchronize();
   for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
   void* ptrs[] = {d->h, d->xn, d->q, d->k, d->v, d->qr, d->attn, d->o, d->gate, d->up, d->act,
-                  d->delta, d->hn, d->logits, d->ids, d->counters, d->part, d->amax, d->arrive};
+                  d->delta, d->hn, d->logits, d->ids, d->counters, d->part, d->amax, d->arrive,
+                  d->rope_table};
   for (void* p : ptrs)
     if (p) hipFree(p);
   if (d->stream) hipStreamDestroy(d->stream);

@@ -77,6 +77,7 @@ struct Q4Batch {
   int head_dim, n_heads, n_kv_heads, lmax, pos0;
   const int* dpos;  // device position (graph-replayed step) or nullptr
   float theta;
+  const float2* rope_table;  // [lmax][head_dim/2] (cos, sin) or nullptr
   uint16_t* q_out;  // [M, Hq, 1, D] bf16
   uint16_t* kc;     // cache layer [M, Hkv, lmax, D] bf16
   uint16_t* vc;
@@ -498,7 +499,13 @@ __global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__
             batch.vc[co + i + half] = f32_to_bf16(a1);
           } else {
             float c, sn, o1, o2;
-            rope_cs(pos, i, D, batch.theta, &c, &sn);
+            if (batch.rope_table) {
+              const float2 t = batch.rope_table[(int64_t)pos * half + i];
+              c = t.x;
+              sn = t.y;
+            } else {
+              rope_cs(pos, i, D, batch.theta, &c, &sn);
+            }
             rotate_pair(a0, a1, c, sn, &o1, &o2);
             if (e_pid[0] == 0) {
               const int64_t qo = ((int64_t)m * batch.n_heads + h) * D;
@@ -646,11 +653,16 @@ GemvShape pick_shape(int nv, int rows, int M) {
 }
 
 // Persistent grid size: workgroups per CU times CUs (STRATA_GEMV_WGS_PER_CU
-// overrides the per-CU count).
+// overrides the per-CU count).  Long rows (U >= 7: K >= 12k) stage a large x
+// per workgroup, so they run one workgroup per CU over several row blocks.
 int g_num_cus = 256;
-int grid_cap(int nw) {
-  int per_cu = nw >= 8 ? 2 : 4;
+int grid_cap(int nw, int u, bool norm) {
+  int per_cu = u >= 7 ? 1 : (nw >= 8 ? 2 : 4);
   if (const char* e = getenv("STRATA_GEMV_WGS_PER_CU")) per_cu = atoi(e);
+  if (norm) {
+    per_cu = 4;
+    if (const char* e = getenv("STRATA_GEMV_NORM_WGS_PER_CU")) per_cu = atoi(e);
+  }
   return std::max(1, per_cu) * g_num_cus;
 }
 
@@ -658,7 +670,7 @@ template <int NW, int R, int U, int MT, int EPI, bool NORM, typename XT, typenam
 void launch_q4_k(const void* x, int M, int K, const Q4Batch& batch, const NormArgs& na,
                  size_t lds, hipStream_t stream) {
   const int nblk = (batch.total_rows + NW * R - 1) / (NW * R);
-  dim3 grid(std::min(nblk, grid_cap(NW)), (M + MT - 1) / MT);
+  dim3 grid(std::min(nblk, grid_cap(NW, U, NORM)), (M + MT - 1) / MT);
   const int items = MT * (K / 32), threads = NW * 64;
   const XT* xx = reinterpret_cast<const XT*>(x);
   if (sizeof(XT) == 2 && items <= threads)

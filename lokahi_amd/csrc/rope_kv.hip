@@ -179,3 +179,26 @@ int strata_rope_kv_fused_launch(const void* qs, const void* ks, const void* vs, 
   STRATA_HIP_CHECK(hipGetLastError());
   return STRATA_OK;
 }
+
+namespace {
+__global__ void rope_table_kernel(float2* __restrict__ table, int lmax, int D, float theta) {
+  const int half = D >> 1;
+  const int64_t n = (int64_t)lmax * half;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int pos = static_cast<int>(idx / half), i = static_cast<int>(idx % half);
+    float c, s;
+    rope_cs(pos, i, D, theta, &c, &s);
+    table[idx] = make_float2(c, s);
+  }
+}
+}  // namespace
+
+int strata_rope_table_launch(float2* table, int lmax, int D, float theta, void* stream) {
+  const int64_t n = (int64_t)lmax * (D / 2);
+  const int blocks = static_cast<int>(std::min<int64_t>((n + 255) / 256, 4096));
+  hipLaunchKernelGGL(rope_table_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), table, lmax,
+                     D, theta);
+  STRATA_HIP_CHECK(hipGetLastError());
+  return STRATA_OK;
+}

@@ -24,6 +24,7 @@ struct GemvEpilogue {
   uint16_t* vc;
   const uint16_t* norm_w;
   float eps;
+  const float2* rope_table;  // optional (cos, sin) table [lmax][head_dim/2] for mode 2
 };
 int strata_q4_gemv_epi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
                        int count, const GemvEpilogue& e, void* stream);
@@ -60,6 +61,9 @@ int strata_argmax_launch(const float* logits, int64_t rows, int64_t V, float tem
                          int32_t* out, void* partial, void* stream);
 int strata_quantize_launch(const void* src, int dtype, int64_t N, int64_t K, int G, uint32_t* w,
                            uint16_t* s, uint16_t* b, void* stream);
+// (cos, sin) of RoPE for positions 0..lmax-1 and pairs 0..D/2-1, evaluated
+// exactly as the in-kernel RoPE evaluates them (bit-identical).
+int strata_rope_table_launch(float2* table, int lmax, int D, float theta, void* stream);
 int strata_decode_advance_launch(const int32_t* ids, int B, int32_t* out_tokens, int out_stride,
                                  int* counters, void* stream);
 
