@@ -24,6 +24,7 @@ int strata_q4_gemv_epi(strata_ctx* ctx, const void* x, int M, int K, const strat
     batch.pos0 = e.pos0;
     batch.dpos = e.dpos;
     batch.theta = e.theta;
+    STRATA_REQUIRE(e.rope_table != nullptr, "RoPE/KV epilogue needs the (cos, sin) table");
     batch.rope_table = e.rope_table;
     batch.q_out = e.q_out;
     batch.kc = e.kc;

@@ -77,7 +77,7 @@ struct Q4Batch {
   int head_dim, n_heads, n_kv_heads, lmax, pos0;
   const int* dpos;  // device position (graph-replayed step) or nullptr
   float theta;
-  const float2* rope_table;  // [lmax][head_dim/2] (cos, sin) or nullptr
+  const float2* rope_table;  // [lmax][head_dim/2] (cos, sin) of every cache position
   uint16_t* q_out;  // [M, Hq, 1, D] bf16
   uint16_t* kc;     // cache layer [M, Hkv, lmax, D] bf16
   uint16_t* vc;
@@ -322,6 +322,13 @@ __global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__
   // Row block blk = NW*R rows: wave w owns rows (blk*NW + w)*R + r.
   const int nblk = (batch.total_rows + NW * R - 1) / (NW * R);
   int blk = blockIdx.x;
+  // Epilogue operands are fetched with the block's weights, not at the tail:
+  // the RoPE position and (cos, sin) of the block's pair, and the residual
+  // values h[m, n] the RESID epilogue adds to.
+  int rope_pos = 0;
+  if constexpr (EPI == EPI_ROPE_KV) rope_pos = batch.dpos ? *batch.dpos : batch.pos0;
+  float2 cs_pre = make_float2(0.f, 0.f);
+  uint16_t h_pre[R][MT];
   auto setup = [&](int b) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -346,7 +353,22 @@ __global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__
     wp[r] = batch.p[pi].w + (int64_t)n * nv;
     sp[r] = batch.p[pi].s + (int64_t)n * (nv >> 1);
     bp[r] = batch.p[pi].b + (int64_t)n * (nv >> 1);
+    if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+      for (int mm = 0; mm < MT; ++mm) {
+        const int m = min(m0 + mm, M - 1);
+        h_pre[r][mm] = reinterpret_cast<const uint16_t*>(batch.p[pi].y)[(int64_t)m * batch.p[pi].n + n];
+      }
+    }
   }
+  };
+  // The (cos, sin) load depends on the position load: issue it after the
+  // block's weight loads so they do not queue behind it.
+  auto prefetch_rope = [&]() {
+    if constexpr (EPI == EPI_ROPE_KV) {
+      const int D = batch.head_dim, i = nloc[0] % D;  // pair (i, i + D/2), i < D/2
+      cs_pre = batch.rope_table[(int64_t)rope_pos * (D >> 1) + min(i, (D >> 1) - 1)];
+    }
   };
   setup(blk);
 
@@ -441,12 +463,14 @@ __global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__
     XStage<MT, XI> st;
     xstage_load<MT, XI>(st, reinterpret_cast<const uint16_t*>(x), M, K, m0, nv);
     issue(0);
+    prefetch_rope();
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (NORM) xstage_norm<NW, MT, XI>(st, M, K, m0, nv, na);
     xstage_store<MT, XI>(st, M, m0, nv, smem);
   } else {
     stage_x<XT, MT>(x, M, K, m0, smem, nv);
     issue(0);
+    prefetch_rope();
   }
   __syncthreads();
   // Persistent over row blocks (grid-stride): x is staged once per
@@ -460,17 +484,22 @@ __global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__
   }
   int e_pid[R], e_nloc[R];
   bool e_valid[R];
+  uint16_t e_h[R][MT];
+  const float2 e_cs = cs_pre;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     e_pid[r] = pid[r];
     e_nloc[r] = nloc[r];
     e_valid[r] = valid[r];
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) e_h[r][mm] = h_pre[r][mm];
   }
   const int next = blk + gridDim.x;
   const bool more = next < nblk;
   if (more) {
     setup(next);
     issue(0);
+    prefetch_rope();
   }
 
 #pragma unroll
@@ -492,20 +521,14 @@ __global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__
         } else {
           const int D = batch.head_dim, half = D >> 1;
           const int h = e_nloc[0] / D, i = e_nloc[0] - h * D;  // i < D/2: pair (i, i + D/2)
-          const int pos = batch.dpos ? *batch.dpos : batch.pos0;
+          const int pos = rope_pos;
           if (e_pid[0] == 2) {  // v: copy into the cache
             const int64_t co = (((int64_t)m * batch.n_kv_heads + h) * batch.lmax + pos) * D;
             batch.vc[co + i] = f32_to_bf16(a0);
             batch.vc[co + i + half] = f32_to_bf16(a1);
           } else {
-            float c, sn, o1, o2;
-            if (batch.rope_table) {
-              const float2 t = batch.rope_table[(int64_t)pos * half + i];
-              c = t.x;
-              sn = t.y;
-            } else {
-              rope_cs(pos, i, D, batch.theta, &c, &sn);
-            }
+            const float c = e_cs.x, sn = e_cs.y;
+            float o1, o2;
             rotate_pair(a0, a1, c, sn, &o1, &o2);
             if (e_pid[0] == 0) {
               const int64_t qo = ((int64_t)m * batch.n_heads + h) * D;
@@ -531,7 +554,7 @@ __global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__
         if constexpr (EPI == EPI_RESID) {
           uint16_t* hp = reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * p.n + e_nloc[r];
           const float o = bf16_to_f32(f32_to_bf16(acc[r][mm]));
-          *hp = f32_to_bf16(bf16_to_f32(*hp) + o);
+          *hp = f32_to_bf16(bf16_to_f32(e_h[r][mm]) + o);
         } else {
           store_y<YT>(p.y, (int64_t)m * p.n + e_nloc[r], acc[r][mm]);
         }
@@ -745,7 +768,6 @@ int dispatch_q4(strata_ctx* ctx, const void* x, int M, int K, const Q4Batch& bat
     else if (g.nw == 4 && g.r == 1) ok = launch_q4_u<4, 1, 1, EPI, NORM, XT, YT>(g, x, M, K, batch, na, lds, stream);
     else if (g.nw == 8 && g.r == 1) ok = launch_q4_u<8, 1, 1, EPI, NORM, XT, YT>(g, x, M, K, batch, na, lds, stream);
     else if (g.nw == 8 && g.r == 2) ok = launch_q4_u<8, 2, 1, EPI, NORM, XT, YT>(g, x, M, K, batch, na, lds, stream);
-    else if (g.nw == 16 && g.r == 1) ok = launch_q4_u<16, 1, 1, EPI, NORM, XT, YT>(g, x, M, K, batch, na, lds, stream);
   }
   if (!ok)
     return strata_set_error(STRATA_EINVAL, "q4 GEMV: no kernel for geometry nw=%d r=%d u=%d mt=%d",

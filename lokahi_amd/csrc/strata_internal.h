@@ -24,7 +24,7 @@ struct GemvEpilogue {
   uint16_t* vc;
   const uint16_t* norm_w;
   float eps;
-  const float2* rope_table;  // optional (cos, sin) table [lmax][head_dim/2] for mode 2
+  const float2* rope_table;  // (cos, sin) table [lmax][head_dim/2], required by mode 2
 };
 int strata_q4_gemv_epi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
                        int count, const GemvEpilogue& e, void* stream);
