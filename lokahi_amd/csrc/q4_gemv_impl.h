@@ -666,7 +666,7 @@ GemvShape pick_shape(int nv, int rows, int M) {
     g.nw = rows < 8192 ? 8 : 4;
     g.r = rows < 8192 ? 1 : 2;
   } else {
-    g.nw = g.u == 4 ? 4 : 8;
+    g.nw = 4;  // K >= 8k: 4 waves, one row each (K=14336 measured 10.2 us vs 11.1 with 8)
     g.r = 1;
   }
   if (const char* e = getenv("STRATA_GEMV_NW")) g.nw = atoi(e);
@@ -677,10 +677,11 @@ GemvShape pick_shape(int nv, int rows, int M) {
 
 // Persistent grid size: workgroups per CU times CUs (STRATA_GEMV_WGS_PER_CU
 // overrides the per-CU count).  Long rows (U >= 7: K >= 12k) stage a large x
-// per workgroup, so they run one workgroup per CU over several row blocks.
+// per workgroup, so they run three 4-wave workgroups per CU over several row
+// blocks.
 int g_num_cus = 256;
 int grid_cap(int nw, int u, bool norm) {
-  int per_cu = u >= 7 ? 1 : (nw >= 8 ? 2 : 4);
+  int per_cu = u >= 7 ? 3 : (nw >= 8 ? 2 : 4);
   if (const char* e = getenv("STRATA_GEMV_WGS_PER_CU")) per_cu = atoi(e);
   if (norm) {
     per_cu = 4;
