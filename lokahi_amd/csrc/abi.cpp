@@ -79,6 +79,7 @@ int strata_ctx_destroy(strata_ctx* ctx) {
   if (!ctx) return STRATA_OK;
   hipDeviceSynchronize();
   if (ctx->scratch) hipFree(ctx->scratch);
+  strata_gemm_lt_destroy(ctx);
   delete ctx;
   return STRATA_OK;
 }
@@ -116,9 +117,8 @@ int strata_linear_q4_multi(strata_ctx* ctx, const void* x, int x_dtype, int64_t 
   if (M == 0) return STRATA_OK;
   if (M > 8 && x_dtype == STRATA_BF16) {
     for (int i = 0; i < count; ++i) {
-      rc = strata_q4_gemm_launch(x, (int)M, (int)K, weights[i].w, weights[i].scales,
-                                 weights[i].biases, (int)weights[i].N, weights[i].y, y_dtype,
-                                 stream);
+      rc = strata_q4_gemm(ctx, x, (int)M, (int)K, weights[i].w, weights[i].scales,
+                          weights[i].biases, (int)weights[i].N, weights[i].y, y_dtype, stream);
       if (rc) return rc;
     }
     return STRATA_OK;

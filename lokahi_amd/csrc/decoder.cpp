@@ -146,7 +146,7 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
     void* kc = kv->kl(li);
     void* vc = kv->vl(li);
     for (auto& w : qkv)
-      RC(strata_q4_gemm_launch(d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
+      RC(strata_q4_gemm(d->ctx, d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
                                stream));
     RC(strata_rope_kv_fused_launch(d->q, d->k, d->v, STRATA_BF16, B, Hq, Hkv, L, D, kv->Lmax,
                                    pos0, nullptr, c.rope_theta, d->qr, kc, vc, STRATA_BF16,
@@ -158,19 +158,19 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
                                  d->attn, ex, stream));
     strata_q4_weight o = Lw.o;
     o.y = d->o;
-    RC(strata_q4_gemm_launch(d->attn, T, Hq * D, o.w, o.scales, o.biases, (int)o.N, o.y,
+    RC(strata_q4_gemm(d->ctx, d->attn, T, Hq * D, o.w, o.scales, o.biases, (int)o.N, o.y,
                              STRATA_BF16, stream));
     RC(strata_rmsnorm_launch(d->h, d->o, Lw.post_norm, T, H, c.rms_norm_eps, d->xn, stream));
     strata_q4_weight gu[2] = {Lw.gate, Lw.up};
     gu[0].y = d->gate;
     gu[1].y = d->up;
     for (auto& w : gu)
-      RC(strata_q4_gemm_launch(d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
+      RC(strata_q4_gemm(d->ctx, d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
                                stream));
     RC(strata_silu_mul_launch(d->gate, d->up, (int64_t)T * F, d->act, stream));
     strata_q4_weight dn = Lw.down;
     dn.y = d->delta;
-    RC(strata_q4_gemm_launch(d->act, T, F, dn.w, dn.scales, dn.biases, (int)dn.N, dn.y,
+    RC(strata_q4_gemm(d->ctx, d->act, T, F, dn.w, dn.scales, dn.biases, (int)dn.N, dn.y,
                              STRATA_BF16, stream));
   }
   // final norm of h + delta, then lm_head on the last position of each row

@@ -1,0 +1,201 @@
+// Prefill q4 linear for long prompts: dequantize, then a library bf16 GEMM.
+//
+// Same maths as mx.quantized_matmul(transpose=True) (src/ollm/llama_mlx.py:53-74)
+// on the prefill path.  At prefill sizes the GEMM is compute-bound and the
+// weight is tiny next to it (gate projection of an 8B model at 8192 tokens:
+// 29 MB of codes against 0.96 TFLOP), so the weight is expanded ONCE per call
+// into a bf16 [N, K] tile (s*q + b in fp32, round-to-nearest-even: the values
+// the fused kernel stages in LDS, bit for bit) and the product runs on
+// hipBLASLt's tuned gfx950 MFMA kernels with fp32 accumulation.  The expansion
+// is one HBM pass (K/2 bytes read, 2K written per row) and costs ~1-3% of the
+// GEMM at 8k tokens.
+//
+// Layout: row-major Y[M, N] = X[M, K] W[N, K]^T is column-major
+// Y^T (N x M, ld N) = op_T(W as K x N, ld K) * op_N(X^T as K x M, ld K).
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <cstdlib>
+#include <map>
+#include <tuple>
+
+#include "strata_common.h"
+#include "strata_internal.h"
+
+namespace {
+
+// One thread expands 32 codes (one uint4 of packed words) into 64 bytes of bf16.
+__global__ __launch_bounds__(256) void q4_dequant_bf16_kernel(const uint4* __restrict__ w,
+                                                              const uint16_t* __restrict__ sc,
+                                                              const uint16_t* __restrict__ bi,
+                                                              int64_t n_chunks, int chunks_per_row,
+                                                              uint4* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n_chunks) return;
+  const int64_t row = i / chunks_per_row;
+  const int c = (int)(i - row * chunks_per_row);
+  const int groups = chunks_per_row >> 1;  // two chunks per group of 64
+  const uint4 u4 = load_nt(w + i);
+  const float s = bf16_to_f32(sc[row * groups + (c >> 1)]);
+  const float b = bf16_to_f32(bi[row * groups + (c >> 1)]);
+  const uint32_t words[4] = {u4.x, u4.y, u4.z, u4.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t lo = words[j] & 0x0f0f0f0fu;          // codes 0, 2, 4, 6
+    const uint32_t hi = (words[j] >> 4) & 0x0f0f0f0fu;   // codes 1, 3, 5, 7
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = fmaf(s, static_cast<float>((lo >> (8 * e)) & 0xffu), b);
+      const float d = fmaf(s, static_cast<float>((hi >> (8 * e)) & 0xffu), b);
+      const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(d)};
+      o[e] = __builtin_bit_cast(uint32_t, v);
+    }
+    out[i * 4 + j] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+constexpr size_t kLtWorkspace = 64u << 20;
+
+struct Plan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  bool ok = false;
+};
+
+}  // namespace
+
+struct GemmLt {
+  hipblasLtHandle_t handle = nullptr;
+  void* workspace = nullptr;
+  void* wdq = nullptr;  // bf16 weight tile [N, K]
+  size_t wdq_bytes = 0;
+  std::map<std::tuple<int, int, int, int>, Plan> plans;
+};
+
+namespace {
+
+// Read per call (a prefill GEMM runs for tens of microseconds at least), so a
+// process can switch paths; 0 or a negative value disables the library path.
+int lt_min_rows() {
+  const char* e = std::getenv("STRATA_GEMM_LT_MIN_M");
+  return e ? std::atoi(e) : 256;
+}
+
+#define LT_CHECK(expr)                                                              \
+  do {                                                                              \
+    hipblasStatus_t _s = (expr);                                                    \
+    if (_s != HIPBLAS_STATUS_SUCCESS)                                               \
+      return strata_set_error(STRATA_EHIP, "%s failed: status %d", #expr, (int)_s); \
+  } while (0)
+
+int lt_init(strata_ctx* ctx) {
+  if (ctx->lt) return STRATA_OK;
+  auto* lt = new GemmLt();
+  if (hipblasLtCreate(&lt->handle) != HIPBLAS_STATUS_SUCCESS) {
+    delete lt;
+    return strata_set_error(STRATA_EHIP, "hipblasLtCreate failed");
+  }
+  if (hipMalloc(&lt->workspace, kLtWorkspace) != hipSuccess) {
+    hipblasLtDestroy(lt->handle);
+    delete lt;
+    return strata_set_error(STRATA_ENOMEM, "GEMM workspace allocation failed");
+  }
+  ctx->lt = lt;
+  return STRATA_OK;
+}
+
+int lt_plan(GemmLt* lt, int M, int N, int K, int y_dtype, Plan** out) {
+  auto key = std::make_tuple(M, N, K, y_dtype);
+  auto it = lt->plans.find(key);
+  if (it != lt->plans.end()) {
+    *out = &it->second;
+    return STRATA_OK;
+  }
+  Plan p;
+  const hipDataType yt = y_dtype == STRATA_F32 ? HIP_R_32F : HIP_R_16BF;
+  LT_CHECK(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
+  const int32_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
+  LT_CHECK(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT)));
+  LT_CHECK(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN)));
+  LT_CHECK(hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, K, N, K));
+  LT_CHECK(hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, K, M, K));
+  LT_CHECK(hipblasLtMatrixLayoutCreate(&p.c, yt, N, M, N));
+  hipblasLtMatmulPreference_t pref;
+  LT_CHECK(hipblasLtMatmulPreferenceCreate(&pref));
+  const uint64_t ws = kLtWorkspace;
+  LT_CHECK(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                 &ws, sizeof(ws)));
+  hipblasLtMatmulHeuristicResult_t heur[1];
+  int found = 0;
+  hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(lt->handle, p.desc, p.a, p.b, p.c, p.c,
+                                                       pref, 1, heur, &found);
+  hipblasLtMatmulPreferenceDestroy(pref);
+  p.ok = st == HIPBLAS_STATUS_SUCCESS && found > 0 && heur[0].workspaceSize <= kLtWorkspace;
+  if (p.ok) p.algo = heur[0].algo;
+  auto ins = lt->plans.emplace(key, p);
+  *out = &ins.first->second;
+  return STRATA_OK;
+}
+
+}  // namespace
+
+void strata_gemm_lt_destroy(strata_ctx* ctx) {
+  GemmLt* lt = ctx->lt;
+  if (!lt) return;
+  for (auto& kv : lt->plans) {
+    Plan& p = kv.second;
+    if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
+    if (p.b) hipblasLtMatrixLayoutDestroy(p.b);
+    if (p.c) hipblasLtMatrixLayoutDestroy(p.c);
+    if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+  }
+  if (lt->wdq) (void)hipFree(lt->wdq);
+  if (lt->workspace) (void)hipFree(lt->workspace);
+  if (lt->handle) hipblasLtDestroy(lt->handle);
+  delete lt;
+  ctx->lt = nullptr;
+}
+
+int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t* w,
+                   const uint16_t* s, const uint16_t* b, int N, void* y, int y_dtype,
+                   void* stream) {
+  const int min_rows = lt_min_rows();
+  if (min_rows <= 0 || M < min_rows)
+    return strata_q4_gemm_launch(x, M, K, w, s, b, N, y, y_dtype, stream);
+  int rc = lt_init(ctx);
+  if (rc) return rc;
+  GemmLt* lt = ctx->lt;
+  Plan* p = nullptr;
+  rc = lt_plan(lt, M, N, K, y_dtype, &p);
+  if (rc) return rc;
+  if (!p->ok)  // no library kernel for this shape: the fused-dequant kernel covers it
+    return strata_q4_gemm_launch(x, M, K, w, s, b, N, y, y_dtype, stream);
+
+  const size_t need = (size_t)N * K * 2;
+  if (need > lt->wdq_bytes) {
+    if (lt->wdq) {
+      // The tile may still be read by queued work.
+      STRATA_HIP_CHECK(hipDeviceSynchronize());
+      STRATA_HIP_CHECK(hipFree(lt->wdq));
+      lt->wdq = nullptr;
+      lt->wdq_bytes = 0;
+    }
+    if (hipMalloc(&lt->wdq, need) != hipSuccess) {
+      lt->wdq = nullptr;
+      return strata_set_error(STRATA_ENOMEM, "bf16 weight tile of %zu bytes failed", need);
+    }
+    lt->wdq_bytes = need;
+  }
+  const int chunks_per_row = K / 32;
+  const int64_t n_chunks = (int64_t)N * chunks_per_row;
+  hipLaunchKernelGGL(q4_dequant_bf16_kernel, dim3((unsigned)((n_chunks + 255) / 256)), dim3(256),
+                     0, as_stream(stream), reinterpret_cast<const uint4*>(w), s, b, n_chunks,
+                     chunks_per_row, static_cast<uint4*>(lt->wdq));
+  STRATA_HIP_CHECK(hipGetLastError());
+  const float alpha = 1.f, beta = 0.f;
+  LT_CHECK(hipblasLtMatmul(lt->handle, p->desc, &alpha, lt->wdq, p->a, x, p->b, &beta, y, p->c, y,
+                           p->c, &p->algo, lt->workspace, kLtWorkspace, as_stream(stream)));
+  return STRATA_OK;
+}

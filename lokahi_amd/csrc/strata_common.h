@@ -129,6 +129,7 @@ struct strata_ctx {
   int max_lds_per_block;
   void* scratch;        // device scratch arena (split-K partials), grown on demand
   size_t scratch_bytes;
+  struct GemmLt* lt;    // prefill GEMM state (library handle, plans, bf16 weight tile)
 };
 
 // Returns a device scratch buffer of at least `bytes` (owned by ctx).

@@ -36,6 +36,13 @@ int strata_bf16_gemv(strata_ctx* ctx, const void* x, int M, int K, const uint16_
                      void* y, int y_dtype, void* stream);
 int strata_q4_gemm_launch(const void* x, int M, int K, const uint32_t* w, const uint16_t* s,
                           const uint16_t* b, int N, void* y, int y_dtype, void* stream);
+// Prefill q4 linear (bf16 x, M > 8).  From STRATA_GEMM_LT_MIN_M rows on
+// (default 256) the weight is dequantized once into a bf16 tile owned by ctx
+// and multiplied with hipBLASLt; below it the fused-dequant MFMA kernel runs.
+int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t* w,
+                   const uint16_t* s, const uint16_t* b, int N, void* y, int y_dtype,
+                   void* stream);
+void strata_gemm_lt_destroy(strata_ctx* ctx);
 int strata_attention_dispatch(strata_ctx* ctx, const void* q, int qd, const void* k, int kd,
                               const void* v, int vd, int64_t kv_bs, int64_t kv_hs,
                               const int32_t* qpos, int B, int Hq, int Hkv, int Lq, int Lk, int D,

@@ -100,6 +100,28 @@ def test_gemm_prefill_matches_oracle(dev, M, N, K):
     assert rel_err(y, ref_b) < TOL_F32
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 1000, 1024), (512, 4096, 4096), (257, 96, 64)])
+def test_gemm_library_path_and_fused_kernel_agree(dev, monkeypatch, M, N, K):
+    """Prefill rows >= STRATA_GEMM_LT_MIN_M take dequant + hipBLASLt; fewer take
+    the fused-dequant MFMA kernel.  Both multiply the same bf16 weight values."""
+    from lokahi_amd import ops
+    rng = np.random.default_rng(M + N + K)
+    w, s, b, x = _problem(rng, N, K, M)
+    args = [to_dev(x, dev)] + [to_dev(a, dev) for a in (w, s, b)]
+    ref = q4.quantized_matmul(bf16_bits_to_f32(x), w, s, b)
+    wq = round_bf16(q4.dequantize(w, s, b, 64).astype(np.float32)).astype(np.float64)
+    ref_b = bf16_bits_to_f32(x).astype(np.float64) @ wq.T
+    outs = {}
+    for path, min_m in (("library", "1"), ("fused", "0")):
+        monkeypatch.setenv("STRATA_GEMM_LT_MIN_M", min_m)
+        y32 = to_np_f32(ops.linear(*args, out_dtype=torch.float32))
+        y16 = to_np_f32(ops.linear(*args))
+        assert rel_err(y32, ref_b) < TOL_F32, path
+        assert rel_err(y16, ref) < TOL_BF16, path
+        outs[path] = y32
+    assert rel_err(outs["library"], outs["fused"]) < TOL_F32
+
+
 def test_linear_rejects_bad_parameters(dev):
     from lokahi_amd import ops
     w = torch.zeros((4, 8), dtype=torch.uint32, device=dev)
