@@ -97,9 +97,11 @@ struct Raw {
 // --------------------------------------------------------------- decode (Lq=1)
 // grid (nsplit, Hkv, B), block 256.  Each workgroup reduces one key chunk of
 // one KV head for its G query heads to (m, s, o[D]) per head.  With several
-// chunks the partials go to part [B, Hq, nsplit, D + 2] = (o[0..D), m, s) and
-// attn_decode_merge combines them (the kernel boundary orders the partials'
-// writes before the merge's reads on every XCD).
+// chunks the partials go to `part` and attn_decode_merge combines them (the
+// kernel boundary orders the partials' writes before the merge's reads on
+// every XCD).  Partials of one (b, hq), part_stride(nsplit, D) floats apart:
+// o[nsplit][D], then (m, s)[nsplit] as float2 (16-byte aligned blocks, so the
+// merge fetches them with wide loads in one round trip).
 constexpr int kMaxDecodeSplits = 256;
 
 template <typename TQ, typename TK, typename TV, int D, int G>
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const TQ* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
     int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Hkv, int Lk,
     const int* __restrict__ dlen, int causal, int chunk, int nsplit, float scale, float eps,
-    float* __restrict__ part, int* __restrict__ arrive, TQ* __restrict__ out) {
+    float* __restrict__ part, TQ* __restrict__ out) {
   constexpr int EPL = 16 / sizeof(TK);          // key elements per lane
   constexpr int LPK = D / EPL;                  // lanes per key
   constexpr int KPW = 64 / LPK;                 // keys per wave step
@@ -230,7 +232,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   constexpr int NS = 4 * KPW;
   constexpr int GB = G <= 4 ? G : (G % 4 == 0 ? 4 : G / 2);  // heads per LDS round
   static_assert(G % GB == 0, "head rounds must tile the group");
-  __shared__ float sm_m[NS][GB], sm_s[NS][GB];
+  __shared__ float2 sm_ms[NS][GB];  // (m, s) per stream and head
   __shared__ float sm_o[NS][GB][D];
   const int stream = wave * KPW + sub;
 #pragma unroll
@@ -240,143 +242,108 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       const int g = g0 + gl;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) sm_o[stream][gl][e0 + e] = o[g][e];
-      if (part_idx == 0) {
-        sm_m[stream][gl] = m[g];
-        sm_s[stream][gl] = s[g];
-      }
+      if (part_idx == 0) sm_ms[stream][gl] = make_float2(m[g], s[g]);
     }
     __syncthreads();
+    // All LDS reads of a thread are issued before any is used (one LDS
+    // latency, not one per stream); streams that saw no key have s = 0.
     for (int idx = threadIdx.x; idx < GB * D; idx += 256) {
       const int gl = idx / D, d = idx - gl * D;
+      float2 ms[NS];
+      float ov[NS];
+#pragma unroll
+      for (int w = 0; w < NS; ++w) {
+        ms[w] = sm_ms[w][gl];
+        ov[w] = sm_o[w][gl][d];
+      }
       float mx = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < NS; ++w)
-        if (sm_s[w][gl] > 0.f) mx = fmaxf(mx, sm_m[w][gl]);
+      for (int w = 0; w < NS; ++w) mx = fmaxf(mx, ms[w].y > 0.f ? ms[w].x : -INFINITY);
       float ss = 0.f, oo = 0.f;
 #pragma unroll
       for (int w = 0; w < NS; ++w) {
-        if (sm_s[w][gl] > 0.f) {
-          const float f = exp2f(sm_m[w][gl] - mx);
-          ss = fmaf(sm_s[w][gl], f, ss);
-          oo = fmaf(sm_o[w][gl][d], f, oo);
-        }
+        const float f = ms[w].y > 0.f ? exp2f(ms[w].x - mx) : 0.f;
+        ss = fmaf(ms[w].y, f, ss);
+        oo = fmaf(ov[w], f, oo);
       }
       const int hq = hkv * G + g0 + gl;
       if (nsplit == 1) {
         Elem<TQ>::store(out, ((int64_t)b * Hq + hq) * D + d, oo / fmaxf(ss, eps));
       } else {
-        float* pp = part + (((int64_t)b * Hq + hq) * nsplit + split) * (D + 2);
-        pp[d] = oo;
-        if (d == 0) { pp[D] = mx; pp[D + 1] = ss; }
+        float* pp = part + ((int64_t)b * Hq + hq) * part_stride(nsplit, D);
+        pp[split * D + d] = oo;
+        if (d == 0)
+          *reinterpret_cast<float2*>(pp + nsplit * D + 2 * split) = make_float2(mx, ss);
       }
     }
     if (g0 + GB < G) __syncthreads();
   }
-  if (nsplit == 1 || arrive == nullptr) return;
-
-  // The last workgroup of this (b, hkv) to finish merges the nsplit partials
-  // of its G heads.  Release: partials are written back device-wide before
-  // the arrival count; acquire: the merger's caches are invalidated after it.
-  __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int old = __hip_atomic_fetch_add(&arrive[b * Hkv + hkv], 1, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-    s_last = old == nsplit - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  __shared__ float sw[4][kMaxDecodeSplits];
-  for (int g = wave; g < G; g += 4) {
-    const int64_t bh = (int64_t)b * Hq + hkv * G + g;
-    const float* pp = part + bh * nsplit * (D + 2);
-    float mxg = -INFINITY;
-    for (int i = lane; i < nsplit; i += 64) {
-      const float si = pp[(int64_t)i * (D + 2) + D + 1];
-      const float mi = si > 0.f ? pp[(int64_t)i * (D + 2) + D] : -INFINITY;
-      sw[wave][i] = mi;
-      mxg = fmaxf(mxg, mi);
-    }
-    for (int off = 32; off >= 1; off >>= 1) mxg = fmaxf(mxg, __shfl_xor(mxg, off, 64));
-    float st = 0.f;
-    for (int i = lane; i < nsplit; i += 64) {
-      const float w = sw[wave][i] == -INFINITY ? 0.f : exp2f(sw[wave][i] - mxg);
-      sw[wave][i] = w;
-      st = fmaf(pp[(int64_t)i * (D + 2) + D + 1], w, st);
-    }
-    st = wave_sum(st);
-    __builtin_amdgcn_wave_barrier();
-    const float inv = 1.f / fmaxf(st, eps);
-    constexpr int DL = D / 64;  // head-dim entries per lane
-    float oo[DL];
-#pragma unroll
-    for (int c = 0; c < DL; ++c) oo[c] = 0.f;
-    for (int i0 = 0; i0 < nsplit; i0 += 8) {
-      float pv[8][DL];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int c = 0; c < DL; ++c)
-          pv[u][c] = pp[(int64_t)min(i0 + u, nsplit - 1) * (D + 2) + lane + 64 * c];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (i0 + u < nsplit)
-#pragma unroll
-          for (int c = 0; c < DL; ++c) oo[c] = fmaf(pv[u][c], sw[wave][i0 + u], oo[c]);
-    }
-#pragma unroll
-    for (int c = 0; c < DL; ++c) Elem<TQ>::store(out, bh * D + lane + 64 * c, oo[c] * inv);
-  }
-  // ready for the next launch (graph replays reuse the counters)
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&arrive[b * Hkv + hkv], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// grid (B*Hq), block 256: combine the nsplit partials of one (b, hq).  All
-// (m, s) pairs are loaded in parallel, the weights exp2(m_i - max) computed
-// once in LDS, then each thread sums its head-dim entries over the chunks.
+// grid (B*Hq), block 256: combine the nsplit partials of one (b, hq), 64
+// splits per round.  Lane l of every wave reads (m, s) of split base + l (the
+// max and the sum are wave reductions); thread t reads head-dim entries
+// 4*(t%32)..+4 of the splits base + t/32 + 8r, r < 8, and takes their
+// weights from the owning lanes with a shuffle.  All loads of a round are
+// issued before any is used.  D <= 128.
 template <typename TQ>
 __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict__ part,
                                                          int nsplit, int D, float eps,
                                                          TQ* __restrict__ out) {
-  __shared__ float sw[kMaxDecodeSplits];
-  __shared__ float red[4];
-  __shared__ float s_tot;
+  __shared__ float4 red[4][32];
   const int bh = blockIdx.x;
-  const float* pp = part + (int64_t)bh * nsplit * (D + 2);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float mx = -INFINITY;
-  for (int i = threadIdx.x; i < nsplit; i += 256) {
-    const float si = pp[(int64_t)i * (D + 2) + D + 1];
-    const float mi = si > 0.f ? pp[(int64_t)i * (D + 2) + D] : -INFINITY;
-    sw[i] = mi;
-    mx = fmaxf(mx, mi);
-  }
+  const float* pp = part + (int64_t)bh * part_stride(nsplit, D);
+  const float2* ms = reinterpret_cast<const float2*>(pp + (int64_t)nsplit * D);
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int c4 = t & 31, ig = t >> 5;
+  const int col = 4 * c4 < D ? 4 * c4 : 0;
+  float mx = -INFINITY, ss = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int base = 0; base < nsplit; base += 64) {
+    // indices clamped, values masked afterwards: no load behind a branch
+    float2 my = ms[min(base + lane, nsplit - 1)];
+    if (base + lane >= nsplit) my.y = 0.f;
+    float4 ov[8];
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < nsplit; i += 256) {
-    const float w = sw[i] == -INFINITY ? 0.f : exp2f(sw[i] - mx);
-    sw[i] = w;
-    ss = fmaf(pp[(int64_t)i * (D + 2) + D + 1], w, ss);
+    for (int r = 0; r < 8; ++r)
+      ov[r] = *reinterpret_cast<const float4*>(pp + (int64_t)min(base + ig + 8 * r, nsplit - 1) * D + col);
+    // keep every load of the round ahead of the first use (one round trip)
+    asm volatile("" : "+v"(my.x), "+v"(my.y));
+#pragma unroll
+    for (int r = 0; r < 8; ++r) asm volatile("" : "+v"(ov[r].x), "+v"(ov[r].y), "+v"(ov[r].z), "+v"(ov[r].w));
+    // Branch-free (a branch here lets the compiler sink the o loads past
+    // it): with no key seen yet mb stays -inf and every weight below is 0.
+    const float mb = fmaxf(mx, wave_max(my.y > 0.f ? my.x : -INFINITY));
+    const float mref = mb == -INFINITY ? 0.f : mb;
+    const float alpha = mx == -INFINITY ? 0.f : exp2f(mx - mref);
+    const float w = my.y > 0.f ? exp2f(my.x - mref) : 0.f;  // 0 for splits past nsplit
+    ss = fmaf(ss, alpha, wave_sum(my.y * w));
+    acc.x *= alpha; acc.y *= alpha; acc.z *= alpha; acc.w *= alpha;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const float wr = __shfl(w, ig + 8 * r, 64);
+      acc.x = fmaf(ov[r].x, wr, acc.x);
+      acc.y = fmaf(ov[r].y, wr, acc.y);
+      acc.z = fmaf(ov[r].z, wr, acc.z);
+      acc.w = fmaf(ov[r].w, wr, acc.w);
+    }
+    mx = mb;
   }
-  ss = wave_sum(ss);
-  if (lane == 0) red[wave] = ss;
+  // lanes t and t+32 of a wave hold the same columns
+  acc.x += __shfl_xor(acc.x, 32, 64);
+  acc.y += __shfl_xor(acc.y, 32, 64);
+  acc.z += __shfl_xor(acc.z, 32, 64);
+  acc.w += __shfl_xor(acc.w, 32, 64);
+  if (lane < 32) red[wave][c4] = acc;
   __syncthreads();
-  if (threadIdx.x == 0) s_tot = (red[0] + red[1]) + (red[2] + red[3]);
-  __syncthreads();
-  const float inv = 1.f / fmaxf(s_tot, eps);
-  for (int d = threadIdx.x; d < D; d += 256) {
-    float oo = 0.f;
-#pragma unroll 8
-    for (int i = 0; i < nsplit; ++i) oo = fmaf(pp[(int64_t)i * (D + 2) + d], sw[i], oo);
-    Elem<TQ>::store(out, (int64_t)bh * D + d, oo * inv);
+  if (t < 32 && 4 * c4 < D) {
+    const float inv = 1.f / fmaxf(ss, eps);
+    const float4 a0 = red[0][c4], a1 = red[1][c4], a2 = red[2][c4], a3 = red[3][c4];
+    const int64_t o0 = (int64_t)bh * D + 4 * c4;
+    Elem<TQ>::store(out, o0 + 0, ((a0.x + a1.x) + (a2.x + a3.x)) * inv);
+    Elem<TQ>::store(out, o0 + 1, ((a0.y + a1.y) + (a2.y + a3.y)) * inv);
+    Elem<TQ>::store(out, o0 + 2, ((a0.z + a1.z) + (a2.z + a3.z)) * inv);
+    Elem<TQ>::store(out, o0 + 3, ((a0.w + a1.w) + (a2.w + a3.w)) * inv);
   }
 }
 
@@ -698,25 +665,24 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
       part = ex.part;
     } else {
       void* p = nullptr;
-      const int rc = strata_ctx_scratch(ctx, (size_t)B * Hq * nsplit * (D + 2) * sizeof(float), &p);
+      const int rc = strata_ctx_scratch(ctx, (size_t)B * Hq * part_stride(nsplit, D) * sizeof(float), &p);
       if (rc) return rc;
       part = reinterpret_cast<float*>(p);
     }
   }
   dim3 grid(nsplit, Hkv, B);
-  int* arrive = ex.arrive;
 #define STRATA_DEC(GV)                                                                        \
   if (G == GV)                                                                                \
     hipLaunchKernelGGL((attn_decode_kernel<TQ, TK, TV, D, GV>), grid, dim3(256), 0, stream,   \
                        (const TQ*)q, (const TK*)k, (const TV*)v, kv_bs, kv_hs, qpos, Hq, Hkv, \
-                       Lk, ex.dlen, causal, chunk, nsplit, scale, eps, part, arrive, (TQ*)out);
+                       Lk, ex.dlen, causal, chunk, nsplit, scale, eps, part, (TQ*)out);
   STRATA_DEC(1) else STRATA_DEC(2) else STRATA_DEC(3) else STRATA_DEC(4) else STRATA_DEC(6) else
   STRATA_DEC(8) else
     return strata_set_error(STRATA_ENOTSUP, "decode attention: group size %d not in {1,2,3,4,6,8}",
                             G);
 #undef STRATA_DEC
   STRATA_HIP_CHECK(hipGetLastError());
-  if (nsplit > 1 && arrive == nullptr) {
+  if (nsplit > 1) {
     hipLaunchKernelGGL((attn_decode_merge<TQ>), dim3(B * Hq), dim3(256), 0, stream, part, nsplit,
                        D, eps, (TQ*)out);
     STRATA_HIP_CHECK(hipGetLastError());

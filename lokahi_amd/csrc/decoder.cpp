@@ -43,8 +43,6 @@ struct strata_decoder {
   int* counters;          // {step, position, key count}
   float* part;            // split-K partials for graph-mode decode attention
   int part_splits;
-  int* arrive;            // split-K arrival counters [max_batch * num_kv_heads] (self-resetting)
-  bool fused_merge;       // merge split-K partials in the attention kernel (else a merge launch)
   float2* rope_table;     // (cos, sin) [Lmax][head_dim/2], built once at creation
   void* amax;             // argmax partials [max_batch * kArgmaxBlocks * 8 B]
   hipStream_t stream;     // the decoder's own stream (graph capture / replay)
@@ -111,7 +109,6 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
       AttnExtra ex;
       ex.part = d->part;
       ex.part_splits = d->part_splits;
-      ex.arrive = d->fused_merge ? d->arrive : nullptr;
       if (graph_mode) ex.dlen = d->counters + 2;
       RC(strata_attention_dispatch(d->ctx, d->qr, STRATA_BF16, kc, STRATA_BF16, vc, STRATA_BF16,
                                    kv_bs, kv_hs, nullptr, B, Hq, Hkv, 1,
@@ -245,10 +242,6 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
   d->kv = kv;
   d->max_batch = max_batch;
   d->max_tokens = max_tokens;
-  // The in-kernel merge (last arriving workgroup, device-scope fences) is
-  // slower on MI355X than a separate merge launch; STRATA_ATTN_FUSED_MERGE
-  // enables it.
-  d->fused_merge = getenv("STRATA_ATTN_FUSED_MERGE") != nullptr;
   const size_t T = max_tokens;
   const size_t H = c.hidden_size, F = c.intermediate_size, QW = (size_t)c.num_heads * c.head_dim,
                KW = (size_t)c.num_kv_heads * c.head_dim;
@@ -263,7 +256,6 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
       {reinterpret_cast<void**>(&d->ids), (size_t)max_batch * 4},
       {reinterpret_cast<void**>(&d->counters), 16},
       {&d->amax, (size_t)max_batch * kArgmaxBlocks * 8},
-      {reinterpret_cast<void**>(&d->arrive), (size_t)max_batch * c.num_kv_heads * 4},
       {reinterpret_cast<void**>(&d->rope_table), (size_t)kv->Lmax * (c.head_dim / 2) * 8},
   };
   for (auto& b : bufs)
@@ -271,12 +263,10 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
   d->part_splits = strata_attn_decode_splits(ctx, kv->B, c.num_kv_heads, kv->Lmax);
   if (!rc)
     rc = alloc(reinterpret_cast<void**>(&d->part),
-               (size_t)kv->B * c.num_heads * d->part_splits * (c.head_dim + 2) * 4);
+               (size_t)kv->B * c.num_heads * part_stride(d->part_splits, c.head_dim) * 4);
   if (!rc) rc = strata_rope_table_launch(d->rope_table, kv->Lmax, c.head_dim, c.rope_theta, nullptr);
   if (!rc && hipDeviceSynchronize() != hipSuccess)
     rc = strata_set_error(STRATA_EHIP, "decoder: RoPE table initialisation failed");
-  if (!rc && hipMemset(d->arrive, 0, (size_t)max_batch * c.num_kv_heads * 4) != hipSuccess)
-    rc = strata_set_error(STRATA_EHIP, "decoder: counter initialisation failed");
   if (!rc && hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess)
     rc = strata_set_error(STRATA_EHIP, "decoder: stream creation failed");
   if (rc) {
@@ -292,7 +282,7 @@ int strata_decoder_destroy(strata_decoder* d) {
   hipDeviceSynchronize();
   for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
   void* ptrs[] = {d->h, d->xn, d->q, d->k, d->v, d->qr, d->attn, d->o, d->gate, d->up, d->act,
-                  d->delta, d->hn, d->logits, d->ids, d->counters, d->part, d->amax, d->arrive,
+                  d->delta, d->hn, d->logits, d->ids, d->counters, d->part, d->amax,
                   d->rope_table};
   for (void* p : ptrs)
     if (p) hipFree(p);

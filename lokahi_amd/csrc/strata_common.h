@@ -102,6 +102,16 @@ __device__ __forceinline__ float dpp_sum(float v) {
 
 __device__ __forceinline__ float wave_sum(float v) { return dpp_sum<64>(v); }
 
+// Maximum over the 64 lanes, same DPP pattern as dpp_sum.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+
 template <int W>
 __device__ __forceinline__ float group_sum(float v) { return dpp_sum<W>(v); }
 
@@ -135,14 +145,18 @@ struct strata_ctx {
 // Returns a device scratch buffer of at least `bytes` (owned by ctx).
 int strata_ctx_scratch(strata_ctx* ctx, size_t bytes, void** out);
 
+// Floats of decode split-K partials per (b, query head): o[nsplit][D] then
+// (m, s)[nsplit]; a multiple of 4 (16-byte blocks) for D % 4 == 0.
+__host__ __device__ constexpr int64_t part_stride(int nsplit, int D) {
+  return (int64_t)nsplit * (D + 4);
+}
+
 // Optional inputs of the attention dispatcher used by the decoder engine.
 struct AttnExtra {
   const int* dlen = nullptr;  // device key count (decode; overrides Lk, which is then capacity)
-  float* part = nullptr;      // caller-owned split-K partials [B, Hq, splits, D + 2]
+  float* part = nullptr;      // caller-owned split-K partials, B * Hq * part_stride(splits, D)
   int part_splits = 0;        // splits the partials buffer holds
   int out_tm = 0;             // prefill: write token-major [B, Lq, Hq, D]
-  int* arrive = nullptr;      // decode: zeroed per-(b, kv head) arrival counters [B * Hkv];
-                              // the last split-K workgroup merges in-kernel
 };
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
