@@ -297,12 +297,22 @@ __device__ __forceinline__ void xstage_norm(XStage<MT, XI>& st, int M, int K, in
 // Order of work: x loads, then every weight/scale/bias load of the first K
 // chunk (16-byte non-temporal loads, unconditional with clamped in-bounds
 // addresses so none sits behind a branch), then x is written to LDS while the
-// weights are still in flight, one barrier, the math, the store.  XI > 0
+// weights are still in flight, one barrier, the math, the store.
+//
+// Batch-1 kernels (MT == 1, bf16 x in one staging round) with short row
+// chunks (U <= 2) in the shapes listed by kFiveWaves fit 96 VGPRs without
+// spills: they are built for 5 waves per SIMD and launched 5 workgroups per
+// CU (the extra wave per SIMD hides more load latency).  XI > 0
 // selects that split staging (bf16 x); XI == 0 stages x up front (fp32 x).
 // EPI picks the epilogue at compile time; NORM (XI > 0 only) applies the
 // RMSNorm prologue to x.
+template <int NW, int R, int U, int MT, int XI, int EPI, typename XT>
+constexpr bool kFiveWaves = sizeof(XT) == 2 && XI == 1 && MT == 1 && U <= 2 &&
+                            (R == 1 || (NW == 4 && R == 2 && (EPI == EPI_STORE || EPI == EPI_SILU_PAIR)));
+
 template <int NW, int R, int U, int MT, int XI, int EPI, bool NORM, typename XT, typename YT>
-__global__ __launch_bounds__(NW * 64) void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(kFiveWaves<NW, R, U, MT, XI, EPI, XT> ? 5 : 1)))
+void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
                                                           Q4Batch batch, NormArgs na) {
   static_assert(!NORM || XI > 0, "the RMSNorm prologue needs split bf16 staging");
   static_assert((EPI != EPI_SILU_PAIR && EPI != EPI_ROPE_KV) || R == 2,
@@ -680,32 +690,39 @@ GemvShape pick_shape(int nv, int rows, int M) {
 // per workgroup, so they run three 4-wave workgroups per CU over several row
 // blocks.
 int g_num_cus = 256;
-int grid_cap(int nw, int u, bool norm) {
-  int per_cu = u >= 7 ? 3 : (nw >= 8 ? 2 : 4);
+// Workgroups per CU of the persistent grid (five_waves: the kernel is built
+// for 5 waves per SIMD).
+int grid_cap(int nw, int u, bool norm, bool five_waves) {
+  int per_cu = u >= 7 ? 3 : (nw >= 8 ? 2 : (five_waves ? 5 : 4));
   if (const char* e = getenv("STRATA_GEMV_WGS_PER_CU")) per_cu = atoi(e);
   if (norm) {
-    per_cu = 4;
+    per_cu = five_waves ? 5 : 4;
     if (const char* e = getenv("STRATA_GEMV_NORM_WGS_PER_CU")) per_cu = atoi(e);
   }
   return std::max(1, per_cu) * g_num_cus;
 }
 
+template <int NW, int R, int U, int MT, int XI, int EPI, bool NORM, typename XT, typename YT>
+void launch_q4_x(const XT* x, int M, int K, const Q4Batch& batch, const NormArgs& na, size_t lds,
+                 hipStream_t stream) {
+  const int nblk = (batch.total_rows + NW * R - 1) / (NW * R);
+  constexpr bool five = kFiveWaves<NW, R, U, MT, XI, EPI, XT>;
+  dim3 grid(std::min(nblk, grid_cap(NW, U, NORM, five)), (M + MT - 1) / MT);
+  hipLaunchKernelGGL((q4_gemv_kernel<NW, R, U, MT, XI, EPI, NORM, XT, YT>), grid, dim3(NW * 64),
+                     lds, stream, x, M, K, batch, na);
+}
+
 template <int NW, int R, int U, int MT, int EPI, bool NORM, typename XT, typename YT>
 void launch_q4_k(const void* x, int M, int K, const Q4Batch& batch, const NormArgs& na,
                  size_t lds, hipStream_t stream) {
-  const int nblk = (batch.total_rows + NW * R - 1) / (NW * R);
-  dim3 grid(std::min(nblk, grid_cap(NW, U, NORM)), (M + MT - 1) / MT);
   const int items = MT * (K / 32), threads = NW * 64;
   const XT* xx = reinterpret_cast<const XT*>(x);
   if (sizeof(XT) == 2 && items <= threads)
-    hipLaunchKernelGGL((q4_gemv_kernel<NW, R, U, MT, 1, EPI, NORM, XT, YT>), grid, dim3(threads),
-                       lds, stream, xx, M, K, batch, na);
+    launch_q4_x<NW, R, U, MT, 1, EPI, NORM, XT, YT>(xx, M, K, batch, na, lds, stream);
   else if (sizeof(XT) == 2 && items <= 2 * threads)
-    hipLaunchKernelGGL((q4_gemv_kernel<NW, R, U, MT, 2, EPI, NORM, XT, YT>), grid, dim3(threads),
-                       lds, stream, xx, M, K, batch, na);
+    launch_q4_x<NW, R, U, MT, 2, EPI, NORM, XT, YT>(xx, M, K, batch, na, lds, stream);
   else if constexpr (!NORM)
-    hipLaunchKernelGGL((q4_gemv_kernel<NW, R, U, MT, 0, EPI, false, XT, YT>), grid, dim3(threads),
-                       lds, stream, xx, M, K, batch, na);
+    launch_q4_x<NW, R, U, MT, 0, EPI, false, XT, YT>(xx, M, K, batch, na, lds, stream);
 }
 
 template <int NW, int R, int MT, int EPI, bool NORM, typename XT, typename YT>
