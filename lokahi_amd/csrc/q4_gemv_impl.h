@@ -662,9 +662,11 @@ struct GemvShape {
 // several thousand waves; large-K rows use 8-wave workgroups so the x staged
 // in LDS is shared by more rows.
 GemvShape pick_shape(int nv, int rows, int M) {
-  // Measured on MI355X (rocprof / back-to-back launches, weights cycled past
-  // the 256 MB last-level cache): K=4096 rows prefer 4 waves x 2 rows with
-  // U=2, small launches 8 waves x 1 row; K=14336 prefers 8 waves x 1 row, U=7.
+  // Measured on MI355X (graph-replayed launches, weights cycled past the
+  // 256 MB last-level cache): K=4096 rows prefer 4 waves x 2 rows with U=2,
+  // small launches 8 waves x 1 row; batch-1 K=14336 prefers 8 waves x 1 row
+  // with U=4 over two K chunks, one row block per workgroup (9.9 us against
+  // 10.7 us for 4 waves with U=7 in one chunk).
   GemvShape g;
   const int chunks = (nv + 63) / 64;
   g.u = chunks <= 2 ? 2 : (chunks <= 4 ? 4 : (chunks <= 7 ? 7 : 8));
@@ -676,8 +678,9 @@ GemvShape pick_shape(int nv, int rows, int M) {
     g.nw = rows < 8192 ? 8 : 4;
     g.r = rows < 8192 ? 1 : 2;
   } else {
-    g.nw = 4;  // K >= 8k: 4 waves, one row each (K=14336 measured 10.2 us vs 11.1 with 8)
+    g.nw = 8;
     g.r = 1;
+    g.u = 4;
   }
   if (const char* e = getenv("STRATA_GEMV_NW")) g.nw = atoi(e);
   if (const char* e = getenv("STRATA_GEMV_R")) g.r = atoi(e);
@@ -686,14 +689,14 @@ GemvShape pick_shape(int nv, int rows, int M) {
 }
 
 // Persistent grid size: workgroups per CU times CUs (STRATA_GEMV_WGS_PER_CU
-// overrides the per-CU count).  Long rows (U >= 7: K >= 12k) stage a large x
-// per workgroup, so they run three 4-wave workgroups per CU over several row
-// blocks.
+// overrides the per-CU count).  8-wave launches (small or long-row linears)
+// get one row block per workgroup at the decode shapes; U >= 7 (batched
+// long rows) runs three 4-wave workgroups per CU over several row blocks.
 int g_num_cus = 256;
 // Workgroups per CU of the persistent grid (five_waves: the kernel is built
 // for 5 waves per SIMD).
 int grid_cap(int nw, int u, bool norm, bool five_waves) {
-  int per_cu = u >= 7 ? 3 : (nw >= 8 ? 2 : (five_waves ? 5 : 4));
+  int per_cu = u >= 7 ? 3 : (nw >= 8 ? 6 : (five_waves ? 5 : 4));
   if (const char* e = getenv("STRATA_GEMV_WGS_PER_CU")) per_cu = atoi(e);
   if (norm) {
     per_cu = five_waves ? 5 : 4;
