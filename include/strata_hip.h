@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define STRATA_ABI_VERSION 1
+#define STRATA_ABI_VERSION 2
 
 enum strata_status {
   STRATA_OK = 0,
@@ -179,6 +179,16 @@ int strata_embed(strata_ctx* ctx, const uint16_t* table, int64_t V, int64_t H,
 int strata_argmax(strata_ctx* ctx, const float* logits, int64_t rows, int64_t V,
                   int32_t* out, void* stream);
 
+/* Dequantize a q4 triple [N, K] to bf16: out = bf16(s*q + b), computed in
+ * fp32 with one round-to-nearest-even.  mx.dequantize of an MLX 4-bit
+ * checkpoint's quantized embedding (src/ollm/llama_mlx.py:722-738); a loader
+ * expands the table once and gathers bf16 rows (same values as gathering
+ * then dequantizing).  bits must be 4, group_size 64; w and out 16-byte
+ * aligned. */
+int strata_dequantize_q4(strata_ctx* ctx, const uint32_t* w, const uint16_t* scales,
+                         const uint16_t* biases, int64_t N, int64_t K, int group_size, int bits,
+                         uint16_t* out, void* stream);
+
 /* Quantize fp32/bf16 weights [N,K] to the q4 affine triple with group 64:
  * per group scale = bf16((max-min)/15), bias = bf16(min),
  * q = clip(rint((w - bias)/scale), 0, 15).  The reference consumes
@@ -212,12 +222,21 @@ typedef struct strata_decoder strata_decoder;
 
 /* embed / lm_head bf16 [vocab, hidden]; final_norm bf16 [hidden].  The KV
  * cache must be bf16 with geometry (num_layers, B <= its batch, num_kv_heads,
- * Lmax, head_dim).  max_tokens bounds B * L of one forward call. */
+ * Lmax, head_dim).  max_tokens bounds B * L of one forward call.  lm_head may
+ * be NULL when a q4 head is set with strata_decoder_set_lm_head_q4 before the
+ * first forward. */
 int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
                           const uint16_t* embed, const uint16_t* final_norm,
                           const uint16_t* lm_head, const strata_llama_layer* layers,
                           strata_kv* kv, int max_batch, int max_tokens, strata_decoder** out);
 int strata_decoder_destroy(strata_decoder* dec);
+
+/* Use a q4 triple [vocab, hidden] (group_size of the config) as the final
+ * projection, with fp32 logits: an MLX 4-bit checkpoint's quantized lm_head,
+ * or its quantized embedding when the head is tied to it
+ * (src/ollm/llama_mlx.py:886-910 projects through _linear on the triple).
+ * Replaces any bf16 head; .y is ignored.  Discards captured decode graphs. */
+int strata_decoder_set_lm_head_q4(strata_decoder* dec, const strata_q4_weight* head);
 
 /* One forward over ids int32 [B, L] (device) appended to the KV cache at its
  * current length; writes fp32 logits of the last position, [B, vocab]. */

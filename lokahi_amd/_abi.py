@@ -103,6 +103,9 @@ _SIGS = {
                                C.c_int),
     "strata_decoder_generate": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_float,
                                  C.c_int, C.c_void_p, C.c_void_p], C.c_int),
+    "strata_decoder_set_lm_head_q4": ([C.c_void_p, C.POINTER(Q4Weight)], C.c_int),
+    "strata_dequantize_q4": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
+                              C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_void_p], C.c_int),
 }
 
 EXPORTED = tuple(_SIGS.keys())
@@ -129,7 +132,7 @@ def load(path=None):
             fn = getattr(lib, name)  # AttributeError if an entry point is missing
             fn.argtypes = args
             fn.restype = res
-        if lib.strata_abi_version() != 1:
+        if lib.strata_abi_version() != 2:
             raise OSError("libstrata_hip.so ABI version mismatch")
         if path is None:
             _lib = lib

@@ -353,6 +353,18 @@ int strata_argmax(strata_ctx* ctx, const float* logits, int64_t rows, int64_t V,
   return strata_argmax_launch(logits, rows, V, 1.0f, out, part, stream);
 }
 
+int strata_dequantize_q4(strata_ctx* ctx, const uint32_t* w, const uint16_t* scales,
+                         const uint16_t* biases, int64_t N, int64_t K, int group_size, int bits,
+                         uint16_t* out, void* stream) {
+  STRATA_REQUIRE(ctx && w && scales && biases && out, "null pointer");
+  STRATA_REQUIRE(bits == 4, "only 4-bit quantization is supported (got bits=%d)", bits);
+  STRATA_REQUIRE(group_size == 64, "only group_size 64 is supported (got %d)", group_size);
+  STRATA_REQUIRE(N >= 0 && K > 0 && K % group_size == 0, "K must be divisible by group_size");
+  STRATA_REQUIRE(K <= INT32_MAX && N * (K / 32) <= (int64_t)UINT32_MAX * 256, "shape too large");
+  STRATA_REQUIRE(aligned16(w) && aligned16(out), "w and out must be 16-byte aligned");
+  return strata_q4_dequant_launch(w, scales, biases, N, (int)K, out, stream);
+}
+
 int strata_quantize_q4(strata_ctx* ctx, const void* wsrc, int w_dtype, int64_t N, int64_t K,
                        int group_size, uint32_t* w, uint16_t* scales, uint16_t* biases,
                        void* stream) {

@@ -32,7 +32,8 @@ struct strata_decoder {
   strata_llama_config cfg;
   const uint16_t* embed;
   const uint16_t* final_norm;
-  const uint16_t* lm_head;
+  const uint16_t* lm_head;   // bf16 [vocab, hidden], or null with head_q4 set
+  strata_q4_weight head_q4;  // q4 lm_head (head_q4.w != null selects it)
   std::vector<strata_llama_layer> layers;
   strata_kv* kv;
   int max_batch, max_tokens;
@@ -57,6 +58,20 @@ struct strata_decoder {
 };
 
 namespace {
+
+// logits fp32 [M, vocab] = x bf16 [M, hidden] . lm_head^T: the bf16 head on
+// the dense GEMV, a q4 head (MLX 4-bit checkpoints, possibly tied to the
+// quantized embedding) on the q4 GEMV (llama_mlx.py:886-910).
+int lm_head_launch(strata_decoder* d, const void* x, int M, float* logits, void* stream) {
+  const strata_llama_config& c = d->cfg;
+  if (d->head_q4.w) {
+    strata_q4_weight w = d->head_q4;
+    w.y = logits;
+    return strata_q4_gemv(d->ctx, x, STRATA_BF16, M, c.hidden_size, &w, 1, STRATA_F32, stream);
+  }
+  return strata_bf16_gemv(d->ctx, x, M, c.hidden_size, d->lm_head, c.vocab_size, logits,
+                          STRATA_F32, stream);
+}
 
 int alloc(void** p, size_t bytes) {
   if (hipMalloc(p, bytes) != hipSuccess) {
@@ -129,8 +144,7 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
       RC(strata_q4_gemv_epi(d->ctx, d->act, T, F, &dn, 1, er, stream));
     }
     RC(strata_rmsnorm_launch(d->h, nullptr, d->final_norm, T, H, c.rms_norm_eps, d->hn, stream));
-    return strata_bf16_gemv(d->ctx, d->hn, B, H, d->lm_head, c.vocab_size, d->logits, STRATA_F32,
-                            stream);
+    return lm_head_launch(d, d->hn, B, d->logits, stream);
   }
   for (int li = 0; li < c.num_layers; ++li) {
     const strata_llama_layer& Lw = d->layers[li];
@@ -173,19 +187,20 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
   // final norm of h + delta, then lm_head on the last position of each row
   RC(strata_rmsnorm_launch(d->h, d->delta, d->final_norm, T, H, c.rms_norm_eps, d->hn, stream));
   if (L == 1) {
-    RC(strata_bf16_gemv(d->ctx, d->hn, B, H, d->lm_head, c.vocab_size, d->logits, STRATA_F32,
-                        stream));
+    RC(lm_head_launch(d, d->hn, B, d->logits, stream));
   } else {
     for (int b = 0; b < B; ++b)
-      RC(strata_bf16_gemv(d->ctx, static_cast<char*>(d->hn) + ((int64_t)b * L + L - 1) * H * 2, 1,
-                          H, d->lm_head, c.vocab_size, d->logits + (int64_t)b * c.vocab_size,
-                          STRATA_F32, stream));
+      RC(lm_head_launch(d, static_cast<char*>(d->hn) + ((int64_t)b * L + L - 1) * H * 2, 1,
+                        d->logits + (int64_t)b * c.vocab_size, stream));
   }
   return STRATA_OK;
 }
 
 int check_forward(strata_decoder* d, int B, int L) {
   STRATA_REQUIRE(d != nullptr, "decoder is NULL");
+  STRATA_REQUIRE(d->lm_head != nullptr || d->head_q4.w != nullptr,
+                 "decoder has no lm_head (a bf16 head at creation or a q4 head via "
+                 "strata_decoder_set_lm_head_q4)");
   STRATA_REQUIRE(B >= 1 && B <= d->max_batch && B <= d->kv->B,
                  "batch %d exceeds the decoder/KV-cache batch", B);
   STRATA_REQUIRE(L >= 1 && (int64_t)B * L <= d->max_tokens,
@@ -214,7 +229,7 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
                           const uint16_t* embed, const uint16_t* final_norm,
                           const uint16_t* lm_head, const strata_llama_layer* layers,
                           strata_kv* kv, int max_batch, int max_tokens, strata_decoder** out) {
-  STRATA_REQUIRE(ctx && cfg && embed && final_norm && lm_head && layers && kv && out,
+  STRATA_REQUIRE(ctx && cfg && embed && final_norm && layers && kv && out,
                  "decoder_create: null argument");
   const strata_llama_config& c = *cfg;
   STRATA_REQUIRE(c.num_layers > 0 && c.hidden_size > 0 && c.num_heads > 0 && c.num_kv_heads > 0 &&
@@ -288,6 +303,21 @@ int strata_decoder_destroy(strata_decoder* d) {
     if (p) hipFree(p);
   if (d->stream) hipStreamDestroy(d->stream);
   delete d;
+  return STRATA_OK;
+}
+
+int strata_decoder_set_lm_head_q4(strata_decoder* d, const strata_q4_weight* head) {
+  STRATA_REQUIRE(d != nullptr && head != nullptr, "set_lm_head_q4: null argument");
+  STRATA_REQUIRE(head->w && head->scales && head->biases, "set_lm_head_q4: null weight pointer");
+  STRATA_REQUIRE(head->N == d->cfg.vocab_size, "set_lm_head_q4: head has %lld rows, vocab is %d",
+                 (long long)head->N, d->cfg.vocab_size);
+  STRATA_REQUIRE(aligned16(head->w), "set_lm_head_q4: packed weights must be 16-byte aligned");
+  // captured decode steps hold the previous head
+  STRATA_HIP_CHECK(hipStreamSynchronize(d->stream));
+  for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
+  d->graphs.clear();
+  d->head_q4 = *head;
+  d->head_q4.y = nullptr;
   return STRATA_OK;
 }
 

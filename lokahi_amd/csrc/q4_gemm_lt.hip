@@ -141,6 +141,18 @@ int lt_plan(GemmLt* lt, int M, int N, int K, int y_dtype, Plan** out) {
 
 }  // namespace
 
+int strata_q4_dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, int64_t N,
+                             int K, uint16_t* out, void* stream) {
+  const int chunks_per_row = K / 32;
+  const int64_t n_chunks = N * chunks_per_row;
+  if (n_chunks == 0) return STRATA_OK;
+  hipLaunchKernelGGL(q4_dequant_bf16_kernel, dim3((unsigned)((n_chunks + 255) / 256)), dim3(256),
+                     0, as_stream(stream), reinterpret_cast<const uint4*>(w), s, b, n_chunks,
+                     chunks_per_row, reinterpret_cast<uint4*>(out));
+  STRATA_HIP_CHECK(hipGetLastError());
+  return STRATA_OK;
+}
+
 void strata_gemm_lt_destroy(strata_ctx* ctx) {
   GemmLt* lt = ctx->lt;
   if (!lt) return;
@@ -188,12 +200,8 @@ int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t*
     }
     lt->wdq_bytes = need;
   }
-  const int chunks_per_row = K / 32;
-  const int64_t n_chunks = (int64_t)N * chunks_per_row;
-  hipLaunchKernelGGL(q4_dequant_bf16_kernel, dim3((unsigned)((n_chunks + 255) / 256)), dim3(256),
-                     0, as_stream(stream), reinterpret_cast<const uint4*>(w), s, b, n_chunks,
-                     chunks_per_row, static_cast<uint4*>(lt->wdq));
-  STRATA_HIP_CHECK(hipGetLastError());
+  rc = strata_q4_dequant_launch(w, s, b, N, K, static_cast<uint16_t*>(lt->wdq), stream);
+  if (rc) return rc;
   const float alpha = 1.f, beta = 0.f;
   LT_CHECK(hipblasLtMatmul(lt->handle, p->desc, &alpha, lt->wdq, p->a, x, p->b, &beta, y, p->c, y,
                            p->c, &p->algo, lt->workspace, kLtWorkspace, as_stream(stream)));

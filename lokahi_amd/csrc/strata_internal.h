@@ -43,6 +43,10 @@ int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t*
                    const uint16_t* s, const uint16_t* b, int N, void* y, int y_dtype,
                    void* stream);
 void strata_gemm_lt_destroy(strata_ctx* ctx);
+// bf16 [N, K] = s*q + b (fp32, one RNE rounding) of a q4 triple; K % 64 == 0,
+// w and out 16-byte aligned.
+int strata_q4_dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, int64_t N,
+                             int K, uint16_t* out, void* stream);
 int strata_attention_dispatch(strata_ctx* ctx, const void* q, int qd, const void* k, int kd,
                               const void* v, int vd, int64_t kv_bs, int64_t kv_hs,
                               const int32_t* qpos, int B, int Hq, int Hkv, int Lq, int Lk, int D,

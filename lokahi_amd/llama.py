@@ -9,7 +9,7 @@ Reproduces the reference's model adapter around the replaced ops:
 Every op is a libstrata_hip.so kernel: embedding gather, fused
 residual-add + RMSNorm, one q4 launch for q/k/v and one for gate/up, fused
 RoPE + KV append, split-K (decode) or MFMA (prefill) attention, SiLU*up,
-bf16 lm_head GEMV and device argmax.  Activations are bf16 between ops
+bf16 (or q4) lm_head GEMV and device argmax.  Activations are bf16 between ops
 (the "bf16" dtype flow); logits are fp32.
 """
 from __future__ import annotations
@@ -151,6 +151,8 @@ class HipLlamaForCausalLM:
         hn = ops.rmsnorm(h, self.w["norm"], cfg.rms_norm_eps, residual=delta)
         if logits == "last":
             hn = hn[:, -1:, :].contiguous()
+        if "lm_head.weight" in self.w:  # q4 head (MLX 4-bit checkpoint, maybe tied)
+            return ops.linear(hn, *self._q4("lm_head"), group_size=g, out_dtype=torch.float32)
         return ops.linear(hn, self.w["lm_head"], None, None, out_dtype=torch.float32)
 
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 100,
@@ -239,10 +241,15 @@ class DecoderEngine:
                                  cfg.num_key_value_heads, cfg.head_dim, cfg.group_size,
                                  cfg.rms_norm_eps, cfg.rope_theta)
         h = C.c_void_p()
+        q4_head = "lm_head.weight" in w
         _abi.check(self._lib.strata_decoder_create(
             _ctx(dev), C.byref(ccfg), w["embed_tokens"].data_ptr(), w["norm"].data_ptr(),
-            w["lm_head"].data_ptr(), layers, cache.handle, max_batch, max_tokens, C.byref(h)))
+            None if q4_head else w["lm_head"].data_ptr(), layers, cache.handle, max_batch,
+            max_tokens, C.byref(h)))
         self.handle = h
+        if q4_head:
+            head = q4("lm_head")
+            _abi.check(self._lib.strata_decoder_set_lm_head_q4(h, C.byref(head)))
         self._layers = layers  # keep the struct array alive with the handle
         self.vocab = cfg.vocab_size
         self._outs = {}

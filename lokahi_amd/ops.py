@@ -141,6 +141,20 @@ def quantize(weight: torch.Tensor, group_size: int = 64):
     return packed, sc, bi
 
 
+def dequantize(weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               group_size: int = 64, bits: int = 4) -> torch.Tensor:
+    """bf16 ``[N, K]`` = s*q + b of a q4 triple (``mx.dequantize``,
+    ``src/ollm/llama_mlx.py:722-738``), fp32 math with one RNE rounding."""
+    dev = _dev(weight)
+    N, K = weight.shape[0], weight.shape[1] * 8
+    _check_q4(weight, scales, biases, N, K, group_size, bits)
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=weight.device)
+    check(_lib().strata_dequantize_q4(_ctx(dev), weight.data_ptr(), scales.data_ptr(),
+                                      biases.data_ptr(), N, K, group_size, bits, out.data_ptr(),
+                                      _stream(dev)))
+    return out
+
+
 # -------------------------------------------------------------------- RoPE
 def rope(q: Optional[torch.Tensor], k: Optional[torch.Tensor], position_ids: torch.Tensor,
          theta: float) -> None:

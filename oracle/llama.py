@@ -68,7 +68,15 @@ def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
 
 
 class OracleLlama:
-    """NumPy Llama with q4 linears and bf16 embedding / lm_head."""
+    """NumPy Llama with q4 linears; embedding and lm_head bf16 or q4.
+
+    Weight names: ``embed_tokens`` (bf16 bits) or the triple
+    ``embed_tokens.weight/.scales/.biases`` (gathered rows dequantized and
+    rounded to bf16, as ``mx.dequantize`` returns them, ``llama_mlx.py:722-738``;
+    the exact rounding of MLX's dequantize is parity unpinned: it is taken as
+    one RNE rounding of the exact ``s*q + b``); ``lm_head`` (bf16 bits) or the
+    triple ``lm_head.weight/...``; with neither, the head is tied to the
+    embedding (``llama_mlx.py:886-910``)."""
 
     def __init__(self, cfg: Config, weights: Dict[str, np.ndarray]):
         self.cfg = cfg
@@ -88,7 +96,7 @@ class OracleLlama:
         ids = np.asarray(ids)
         b, L = ids.shape
         hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
-        h = bf16_bits_to_f32(self.w["embed_tokens"][ids])                # [B, L, H]
+        h = self._embed(ids)                                               # [B, L, H]
         active = cache if use_cache else None
         past = active.get_seq_length() if active is not None else 0
         cache_position = np.arange(past, past + L, dtype=np.int32)
@@ -113,9 +121,32 @@ class OracleLlama:
             a = silu_mul(self._lin(xn, p + "gate_proj"), self._lin(xn, p + "up_proj"))
             h = round_bf16(h + self._lin(a, p + "down_proj"))
         hn = rms_norm(h, self.w["norm"], cfg.rms_norm_eps)
-        if "lm_head_f64" not in self._deq:
-            self._deq["lm_head_f64"] = bf16_bits_to_f32(self.w["lm_head"]).astype(np.float64)
-        return (hn.astype(np.float64) @ self._deq["lm_head_f64"].T).astype(np.float32)
+        return self._head(hn)
+
+    def _embed(self, ids: np.ndarray) -> np.ndarray:
+        if "embed_tokens" in self.w:
+            return bf16_bits_to_f32(self.w["embed_tokens"][ids])
+        rows = q4.dequantize(self.w["embed_tokens.weight"][ids.reshape(-1)],
+                             self.w["embed_tokens.scales"][ids.reshape(-1)],
+                             self.w["embed_tokens.biases"][ids.reshape(-1)], self.cfg.group_size)
+        return round_bf16(rows.astype(np.float32)).reshape(*ids.shape, -1)
+
+    def _head(self, hn: np.ndarray) -> np.ndarray:
+        """fp32 logits: bf16 head, q4 head, or the tied embedding (bf16 or q4)."""
+        if "head_f64" not in self._deq:
+            w = self.w
+            if "lm_head" in w:
+                m = bf16_bits_to_f32(w["lm_head"]).astype(np.float64)
+            elif "lm_head.weight" in w:
+                m = q4.dequantize(w["lm_head.weight"], w["lm_head.scales"], w["lm_head.biases"],
+                                  self.cfg.group_size)
+            elif "embed_tokens" in w:
+                m = bf16_bits_to_f32(w["embed_tokens"]).astype(np.float64)
+            else:
+                m = q4.dequantize(w["embed_tokens.weight"], w["embed_tokens.scales"],
+                                  w["embed_tokens.biases"], self.cfg.group_size)
+            self._deq["head_f64"] = m
+        return (hn.astype(np.float64) @ self._deq["head_f64"].T).astype(np.float32)
 
 
 def greedy_generate(model, input_ids: np.ndarray, *, max_new_tokens: int,

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     assert not missing, f"missing exports: {missing}"
     assert set(syms) == set(_abi.EXPORTED), "ctypes signatures out of sync with the header"
     lib.strata_abi_version.restype = C.c_int
-    assert lib.strata_abi_version() == 1
+    assert lib.strata_abi_version() == 2
 
 
 def test_loader_declares_signatures_and_fails_loudly_on_missing_library(tmp_path):
