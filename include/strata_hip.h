@@ -137,6 +137,13 @@ int strata_kv_destroy(strata_kv* kv);
 int strata_kv_append(strata_kv* kv, int layer, const void* k_new, const void* v_new,
                      int src_dtype, int Lnew, int pos0, void* stream);
 
+/* Replace layer's contents with a snapshot k_src/v_src [B,Hkv,L,D]
+ * (src_dtype, converted to the cache dtype) and set its length to L: the
+ * device side of reloading an offloaded layer (MLXKVCache._load_layer_from_disk,
+ * src/ollm/mlx_kvcache.py:222-250). */
+int strata_kv_restore(strata_kv* kv, int layer, const void* k_src, const void* v_src,
+                      int src_dtype, int L, void* stream);
+
 /* Fused decode/prefill step: take the token-major projection outputs
  * q_src [B, L, Hq*D], k_src / v_src [B, L, Hkv*D] (src_dtype, equal to the
  * cache dtype), apply RoPE at positions pos0..pos0+L-1 to q and k, write

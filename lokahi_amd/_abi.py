@@ -103,6 +103,8 @@ _SIGS = {
                                C.c_int),
     "strata_decoder_generate": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_float,
                                  C.c_int, C.c_void_p, C.c_void_p], C.c_int),
+    "strata_kv_restore": ([C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                           C.c_void_p], C.c_int),
     "strata_decoder_set_lm_head_q4": ([C.c_void_p, C.POINTER(Q4Weight)], C.c_int),
     "strata_dequantize_q4": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                               C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_void_p], C.c_int),

@@ -72,12 +72,8 @@ class HipBackend(Backend):
                         **kwargs):
         if config is None:
             raise BackendError("config is required to create HIP KV cache")
-        if cache_dir is not None:
-            # The disk cold tier (mlx_kvcache.py:183-255, 310-367) is not part
-            # of this build; refuse instead of silently ignoring the directory.
-            raise BackendError("HIP KV cache is device-resident; cache_dir is not supported")
         from ..kvcache import HipKVCache
-        return HipKVCache(config, **kwargs)
+        return HipKVCache(config, cache_dir, stats, **kwargs)
 
     def attention_kernel(self):
         from ..ops import attention

@@ -263,6 +263,27 @@ int strata_kv_append(strata_kv* kv, int layer, const void* k_new, const void* v_
   return STRATA_OK;
 }
 
+int strata_kv_restore(strata_kv* kv, int layer, const void* k_src, const void* v_src,
+                      int src_dtype, int L, void* stream) {
+  STRATA_REQUIRE(kv != nullptr, "kv is NULL");
+  STRATA_REQUIRE(layer >= 0 && layer < kv->layers,
+                 "layer_idx %d is outside configured layer count %d", layer, kv->layers);
+  STRATA_REQUIRE(L >= 0 && L <= kv->Lmax, "restored length %d exceeds the cache capacity %d", L,
+                 kv->Lmax);
+  STRATA_REQUIRE(L == 0 || (k_src != nullptr && v_src != nullptr), "null key/value snapshot");
+  STRATA_REQUIRE(dtype_ok(src_dtype), "unknown dtype code");
+  if (L > 0) {
+    int rc = strata_kv_copy_launch(k_src, src_dtype, kv->kl(layer), kv->dtype, kv->B, kv->Hkv, L,
+                                   kv->Lmax, kv->D, 0, stream);
+    if (rc) return rc;
+    rc = strata_kv_copy_launch(v_src, src_dtype, kv->vl(layer), kv->dtype, kv->B, kv->Hkv, L,
+                               kv->Lmax, kv->D, 0, stream);
+    if (rc) return rc;
+  }
+  kv->len[layer] = L;
+  return STRATA_OK;
+}
+
 int strata_rope_kv_append(strata_kv* kv, int layer, const void* q_src, const void* k_src,
                           const void* v_src, int src_dtype, int Hq, int L, int pos0, float theta,
                           void* q_out, void* stream) {
