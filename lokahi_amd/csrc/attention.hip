@@ -355,8 +355,10 @@ __device__ __forceinline__ f32x4_t mfma_f32(float a, float b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Two floats -> packed bf16 pair, round-to-nearest-even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // grid (ceil(Lq/64), Hq, B), block 256: wave w owns query rows qt*64+16w..+16.
@@ -399,6 +401,13 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
   if (grp == 0) atomicMax(&s_kmax, qp + 1);
   __syncthreads();
   const int kmax = causal ? min(Lk, s_kmax) : Lk;
+  // Key tiles below kfull are visible to every row of this wave (no mask).
+  int kfull = row_ok ? (causal ? qp + 1 : Lk) : 0;
+  kfull = min(kfull, __shfl_xor(kfull, 1, 64));
+  kfull = min(kfull, __shfl_xor(kfull, 2, 64));
+  kfull = min(kfull, __shfl_xor(kfull, 4, 64));
+  kfull = min(kfull, __shfl_xor(kfull, 8, 64));
+  kfull = min(kfull, Lk);
 
   const T* qrow = q + (((int64_t)b * Hq + hq) * Lq + (row_ok ? row : 0)) * D;
   const T* kbase = k + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
@@ -434,6 +443,12 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
   constexpr int NCH = KT * D / CH / 256;        // chunks per thread per tile
   static_assert(KT * D / CH % 256 == 0, "tile chunks must divide over the block");
   uint4 kreg[NCH], vreg[NCH];
+  // bf16 V is fetched as 4 keys x 4 head-dim blocks (8 bytes per key) and
+  // transposed in registers (v_perm), so each block is four 8-byte LDS rows
+  // of the [D][KT + VPAD] tile instead of sixteen 2-byte stores.
+  constexpr int NVB = kBF16 ? (KT / 4) * (D / 4) / 256 : 1;  // 4x4 blocks per thread
+  static_assert(!kBF16 || (KT / 4) * (D / 4) % 256 == 0, "V blocks must divide over the block");
+  uint2 vblk[NVB][4];
   // chunk c of the tile -> (key t, element d0): each wave covers 16 keys x 4
   // consecutive 16-byte chunks (64-byte row segments).
   auto tile_slot = [&](int c, int& t, int& d0) {
@@ -442,18 +457,50 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
     d0 = ((blk >> 2) * 4 + (ln >> 4)) * CH;
   };
   static_assert((D / CH) % 4 == 0, "tile_slot needs a multiple of 4 chunks per key");
+  // Keys past Lk read key Lk-1 (clamped, no load behind a branch) and are
+  // zeroed after the loads when the tile runs past the end.
   auto fetch = [&](int kb) {
+    const bool tail = kb + KT > Lk;
 #pragma unroll
     for (int u = 0; u < NCH; ++u) {
       const int c = threadIdx.x + 256 * u;
       int t, d0;
       tile_slot(c, t, d0);
-      const int key = kb + t;
-      kreg[u] = make_uint4(0, 0, 0, 0);
-      vreg[u] = make_uint4(0, 0, 0, 0);
-      if (key < Lk) {
-        kreg[u] = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * D + d0);
-        vreg[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * D + d0);
+      const int key = min(kb + t, Lk - 1);
+      kreg[u] = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * D + d0);
+      if constexpr (!kBF16) vreg[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * D + d0);
+    }
+    if constexpr (kBF16) {
+#pragma unroll
+      for (int u = 0; u < NVB; ++u) {
+        const int blk = threadIdx.x + 256 * u;
+        const int dg = blk % (D / 4), kg = blk / (D / 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = min(kb + 4 * kg + r, Lk - 1);
+          vblk[u][r] = *reinterpret_cast<const uint2*>(vbase + (int64_t)key * D + 4 * dg);
+        }
+      }
+    }
+    if (tail) {
+#pragma unroll
+      for (int u = 0; u < NCH; ++u) {
+        const int c = threadIdx.x + 256 * u;
+        int t, d0;
+        tile_slot(c, t, d0);
+        if (kb + t >= Lk) {
+          kreg[u] = make_uint4(0, 0, 0, 0);
+          if constexpr (!kBF16) vreg[u] = make_uint4(0, 0, 0, 0);
+        }
+      }
+      if constexpr (kBF16) {
+#pragma unroll
+        for (int u = 0; u < NVB; ++u) {
+          const int kg = (threadIdx.x + 256 * u) / (D / 4);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (kb + 4 * kg + r >= Lk) vblk[u][r] = make_uint2(0, 0);
+        }
       }
     }
   };
@@ -465,18 +512,26 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
       const int c = threadIdx.x + 256 * u;
       int t, d0;
       tile_slot(c, t, d0);
-      const uint4 ku = kreg[u], vu = vreg[u];
-      *reinterpret_cast<uint4*>(&ks[t * (D + KPAD) + d0]) = ku;
-      if constexpr (kBF16) {
-        const uint32_t uu[4] = {vu.x, vu.y, vu.z, vu.w};
-        uint16_t* vt = reinterpret_cast<uint16_t*>(vs);
+      *reinterpret_cast<uint4*>(&ks[t * (D + KPAD) + d0]) = kreg[u];
+      if constexpr (!kBF16) *reinterpret_cast<uint4*>(&vs[t * (D + VPAD) + d0]) = vreg[u];
+    }
+    if constexpr (kBF16) {
+      uint16_t* vt = reinterpret_cast<uint16_t*>(vs);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          vt[(d0 + 2 * i) * (KT + VPAD) + t] = static_cast<uint16_t>(uu[i] & 0xffffu);
-          vt[(d0 + 2 * i + 1) * (KT + VPAD) + t] = static_cast<uint16_t>(uu[i] >> 16);
-        }
-      } else {
-        *reinterpret_cast<uint4*>(&vs[t * (D + VPAD) + d0]) = vu;
+      for (int u = 0; u < NVB; ++u) {
+        const int blk = threadIdx.x + 256 * u;
+        const int dg = blk % (D / 4), kg = blk / (D / 4);
+        const uint2* r = vblk[u];
+        // row j of the transposed block: (V[4kg+0..3][4dg+j]) as one uint2
+        const uint32_t lo = 0x05040100u, hi = 0x07060302u;
+        const uint2 o[4] = {
+            make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, lo), __builtin_amdgcn_perm(r[3].x, r[2].x, lo)),
+            make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, hi), __builtin_amdgcn_perm(r[3].x, r[2].x, hi)),
+            make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, lo), __builtin_amdgcn_perm(r[3].y, r[2].y, lo)),
+            make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, hi), __builtin_amdgcn_perm(r[3].y, r[2].y, hi))};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<uint2*>(&vt[(4 * dg + j) * (KT + VPAD) + 4 * kg]) = o[j];
       }
     }
     __syncthreads();
@@ -501,34 +556,60 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
       st[j] = c;
     }
 
-    // ---- online softmax (log2 domain), all state for this lane's query row
+    // ---- online softmax (log2 domain), all state for this lane's query row.
+    // Raw scores are kept; the scale goes into the exponent's FMA
+    // (sl2 > 0, so max(s * sl2) = sl2 * max(s)).  Tiles every row of the
+    // wave sees in full skip the mask.
+    if (kb0 + KT > kfull) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb0 + 16 * j + 4 * grp + i;
+          const bool ok = key < Lk && (!causal || key <= qp) && row_ok;
+          st[j][i] = ok ? st[j][i] : -INFINITY;
+        }
+    }
     float mb = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kb0 + 16 * j + 4 * grp + i;
-        const bool ok = key < Lk && (!causal || key <= qp) && row_ok;
-        st[j][i] = ok ? st[j][i] * sl2 : -INFINITY;
-        mb = fmaxf(mb, st[j][i]);
-      }
+      for (int i = 0; i < 4; ++i) mb = fmaxf(mb, st[j][i]);
     mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
     mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-    const float mn = fmaxf(m_run, mb);
-    const float alpha = (mn == -INFINITY) ? 1.f : exp2f(m_run - mn);
-    float ps = 0.f;
+    const float mn = fmaxf(m_run, mb * sl2);
+    // v_exp_f32 directly (exp2 of the log2-domain score): results below
+    // 2^-126 flush to 0, far under eps; no libm range reduction per score.
+    float alpha, ps = 0.f;
+    if (kb0 + KT <= kfull) {  // every score finite: mn finite
+      alpha = __builtin_amdgcn_exp2f(m_run - mn);
+      const float nmn = -mn;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = (mn == -INFINITY) ? 0.f : exp2f(st[j][i] - mn);
-        st[j][i] = p;
-        ps += p;
-      }
+        for (int i = 0; i < 4; ++i) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(st[j][i], sl2, nmn));
+          st[j][i] = p;
+          ps += p;
+        }
+    } else {  // rows with no visible key yet keep mn = -inf
+      alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
+      const float nmn = -mn;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = (mn == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(fmaf(st[j][i], sl2, nmn));
+          st[j][i] = p;
+          ps += p;
+        }
+    }
     l_run = fmaf(l_run, alpha, ps);
     m_run = mn;
+    if (__any(alpha != 1.f)) {  // the running max of some row moved
 #pragma unroll
-    for (int i = 0; i < DT; ++i) acc[i] *= alpha;
+      for (int i = 0; i < DT; ++i) acc[i] *= alpha;
+    }
 
     // ---- O^T += V^T P^T
     if constexpr (kBF16) {
