@@ -348,6 +348,39 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict
 }
 
 // ----------------------------------------------------------- prefill on MFMA
+// Workgroup wg of the prefill grid -> (query tile, b, kv head, query head).
+// remap: workgroups are dealt to the 8 XCDs round-robin (wg % 8); a group
+// gi of the G query heads of one (query tile, b, kv head) goes to XCD
+// gi % 8 in G consecutive slots of that XCD, groups ordered longest causal
+// query tile first (measured 1.5x on the bf16 two-block kernel at 8k
+// causal).  Otherwise the order is query tile fastest, then head, then
+// batch.  Returns false for the padding of the last round.
+constexpr int kXcds = 8;
+__host__ __device__ inline int prefill_grid(int nqt, int B, int Hkv, int G) {
+  const int groups = nqt * B * Hkv;
+  return (groups + kXcds - 1) / kXcds * kXcds * G;
+}
+__device__ inline bool prefill_item(bool remap, int wg, int nqt, int B, int Hkv, int G, int* qt,
+                                    int* b, int* hkv, int* hq) {
+  if (!remap) {
+    if (wg >= nqt * B * Hkv * G) return false;
+    *qt = wg % nqt;
+    *hq = (wg / nqt) % (Hkv * G);
+    *b = wg / (nqt * Hkv * G);
+    *hkv = *hq / G;
+    return true;
+  }
+  const int xcd = wg % kXcds, slot = wg / kXcds;
+  const int g = slot % G, gi = (slot / G) * kXcds + xcd;
+  if (gi >= nqt * B * Hkv) return false;
+  const int per_tile = B * Hkv;
+  *qt = nqt - 1 - gi / per_tile;
+  const int rest = gi % per_tile;
+  *b = rest / Hkv;
+  *hkv = rest % Hkv;
+  *hq = *hkv * G + g;
+  return true;
+}
 __device__ __forceinline__ f32x4_t mfma_bf16(const bf16x8_t& a, const bf16x8_t& b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -361,23 +394,30 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// grid (ceil(Lq/64), Hq, B), block 256: wave w owns query rows qt*64+16w..+16.
+// 1-D grid, block 256; workgroup -> (query tile qt, b, hq) by prefill_item:
+// the G query heads of one KV head and query tile run on one XCD in
+// consecutive slots (their K/V tiles share that XCD's L2) and the longest
+// causal query tiles are dispatched first.  Wave w owns QB blocks of 16
+// query rows, qt*64*QB + 16*(QB*w + qb) + 0..15.  Every K / V^T operand read from
+// LDS feeds the QB blocks' MFMAs (QB = 2 halves the LDS traffic per flop).
 // MFMA 16x16 layouts used (wave64, gfx950):
 //   A (16 x K): lane l holds row l%16, k-slots (l/16)*KS .. +KS
 //   B (K x 16): lane l holds col l%16, k-slots (l/16)*KS .. +KS
 //   C (16x16) : lane l holds col l%16, rows (l/16)*4 + 0..3
 // with KS = 8 for bf16 16x16x32 and KS = 1 for f32 16x16x4.
-template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_prefill_mfma(
+template <typename T, int D, int QB>
+// Two query blocks per wave need 2 waves per SIMD to hide the tile loads:
+// the VGPR budget is capped there (fits without spills).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 2 ? 2 : 1)))
+void attn_prefill_mfma(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, int64_t kv_bs,
-    int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Hkv, int Lq, int Lk,
+    int64_t kv_hs, const int32_t* __restrict__ qpos, int B, int Hq, int Hkv, int Lq, int Lk,
     int causal, float scale, float eps, int out_tm, T* __restrict__ out) {
   constexpr bool kBF16 = sizeof(T) == 2;
   constexpr int KT = 64;                         // keys per tile
   constexpr int KPAD = kBF16 ? 8 : 4;            // LDS row padding (elements)
-  // bf16 V is stored transposed [D][KT + VPAD]: a row of 68 elements is 34
-  // dwords, so one wave's transposed 2-byte writes (16 keys x 4 chunks, see
-  // tile_slot) land in 32 distinct banks, and 8-byte reads stay aligned.
+  // bf16 V is stored transposed [D][KT + VPAD]: rows of 68 elements (136 B)
+  // keep the 8-byte reads and writes aligned.
   constexpr int VPAD = 4;
   // K tile: [KT][D + KPAD]; V tile: bf16 -> transposed [D][KT + VPAD], f32 -> [KT][D + VPAD]
   constexpr int K_ELEMS = KT * (D + KPAD);
@@ -386,54 +426,71 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
   __shared__ __attribute__((aligned(16))) T vs[V_ELEMS];
   __shared__ int s_kmax;
 
-  const int qt = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
   const int G = Hq / Hkv;
-  const int hkv = hq / G;
+  int qt, b, hkv, hq;
+  if (!prefill_item(QB == 2, blockIdx.x, (Lq + 64 * QB - 1) / (64 * QB), B, Hkv, G, &qt, &b,
+                    &hkv, &hq))
+    return;  // grid padding
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, grp = lane >> 4;
-  const int row = qt * 64 + wave * 16 + col;  // this lane's query row
-  const bool row_ok = row < Lq;
-  int qp = -1;
-  if (row_ok) qp = causal ? (qpos ? qpos[(int64_t)b * Lq + row] : Lk - Lq + row) : Lk - 1;
-
-  if (threadIdx.x == 0) s_kmax = 0;
-  __syncthreads();
-  if (grp == 0) atomicMax(&s_kmax, qp + 1);
-  __syncthreads();
-  const int kmax = causal ? min(Lk, s_kmax) : Lk;
-  // Key tiles below kfull are visible to every row of this wave (no mask).
-  int kfull = row_ok ? (causal ? qp + 1 : Lk) : 0;
+  int row[QB], qp[QB];
+  bool row_ok[QB];
+  int kfull = Lk, kneed = 0;
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    row[qb] = qt * 64 * QB + 16 * (QB * wave + qb) + col;  // this lane's query rows
+    row_ok[qb] = row[qb] < Lq;
+    qp[qb] = -1;
+    if (row_ok[qb])
+      qp[qb] = causal ? (qpos ? qpos[(int64_t)b * Lq + row[qb]] : Lk - Lq + row[qb]) : Lk - 1;
+    kneed = max(kneed, qp[qb] + 1);
+    // key tiles below kfull are visible to every row of this wave (no mask)
+    kfull = min(kfull, row_ok[qb] ? (causal ? qp[qb] + 1 : Lk) : 0);
+  }
   kfull = min(kfull, __shfl_xor(kfull, 1, 64));
   kfull = min(kfull, __shfl_xor(kfull, 2, 64));
   kfull = min(kfull, __shfl_xor(kfull, 4, 64));
   kfull = min(kfull, __shfl_xor(kfull, 8, 64));
-  kfull = min(kfull, Lk);
 
-  const T* qrow = q + (((int64_t)b * Hq + hq) * Lq + (row_ok ? row : 0)) * D;
+  if (threadIdx.x == 0) s_kmax = 0;
+  __syncthreads();
+  if (grp == 0) atomicMax(&s_kmax, kneed);
+  __syncthreads();
+  const int kmax = causal ? min(Lk, s_kmax) : Lk;
+
   const T* kbase = k + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
   const T* vbase = v + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
 
-  // Q fragment as the B operand of S^T = K Q^T: col = query row, k = head dim.
+  // Q fragments as the B operand of S^T = K Q^T: col = query row, k = head dim.
   constexpr int QF = kBF16 ? D / 32 : D / 4;
-  bf16x8_t qb[kBF16 ? QF : 1];
-  float qf[kBF16 ? 1 : QF];
-  if constexpr (kBF16) {
+  bf16x8_t qbf[QB][kBF16 ? QF : 1];
+  float qf[QB][kBF16 ? 1 : QF];
 #pragma unroll
-    for (int s = 0; s < QF; ++s) {
-      uint4 u = make_uint4(0, 0, 0, 0);
-      if (row_ok) u = *reinterpret_cast<const uint4*>(qrow + s * 32 + grp * 8);
-      qb[s] = __builtin_bit_cast(bf16x8_t, u);
+  for (int qb = 0; qb < QB; ++qb) {
+    const T* qrow = q + (((int64_t)b * Hq + hq) * Lq + (row_ok[qb] ? row[qb] : 0)) * D;
+    if constexpr (kBF16) {
+#pragma unroll
+      for (int s = 0; s < QF; ++s) {
+        uint4 u = make_uint4(0, 0, 0, 0);
+        if (row_ok[qb]) u = *reinterpret_cast<const uint4*>(qrow + s * 32 + grp * 8);
+        qbf[qb][s] = __builtin_bit_cast(bf16x8_t, u);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < QF; ++s) qf[qb][s] = row_ok[qb] ? Elem<T>::load(qrow, s * 4 + grp) : 0.f;
     }
-  } else {
-#pragma unroll
-    for (int s = 0; s < QF; ++s) qf[s] = row_ok ? Elem<T>::load(qrow, s * 4 + grp) : 0.f;
   }
 
   constexpr int DT = D / 16;  // output d tiles
-  f32x4_t acc[DT];
+  f32x4_t acc[QB][DT];
+  float m_run[QB], l_run[QB];
 #pragma unroll
-  for (int i = 0; i < DT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
+  for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+    for (int i = 0; i < DT; ++i) acc[qb][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    m_run[qb] = -INFINITY;
+    l_run[qb] = 0.f;
+  }
   const float sl2 = scale * kLog2e;
 
   // K/V tiles are register-prefetched: tile t+1's global loads are issued
@@ -536,79 +593,101 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
     }
     __syncthreads();
     if (kb0 + KT < kmax) fetch(kb0 + KT);
+    // Query blocks of this wave that see any key of the tile (causal: the
+    // wave's later blocks may, its earlier ones may not, near the diagonal).
+    bool live[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      int need = qp[qb] + 1;
+      need = max(need, __shfl_xor(need, 1, 64));
+      need = max(need, __shfl_xor(need, 2, 64));
+      need = max(need, __shfl_xor(need, 4, 64));
+      need = max(need, __shfl_xor(need, 8, 64));
+      live[qb] = kb0 < need;
+    }
 
-    // ---- S^T tiles: st[j][i] = score(query row, key kb0 + 16j + 4*grp + i)
-    f32x4_t st[4];
+    // ---- S^T tiles: st[qb][j][i] = score(query row of block qb, key kb0 + 16j + 4*grp + i)
+    f32x4_t st[QB][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      f32x4_t c = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) st[qb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       if constexpr (kBF16) {
 #pragma unroll
         for (int s = 0; s < QF; ++s) {
           const uint4 a = *reinterpret_cast<const uint4*>(&ks[(16 * j + col) * (D + KPAD) + s * 32 + grp * 8]);
-          c = mfma_bf16(__builtin_bit_cast(bf16x8_t, a), qb[s], c);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+            if (live[qb]) st[qb][j] = mfma_bf16(__builtin_bit_cast(bf16x8_t, a), qbf[qb][s], st[qb][j]);
         }
       } else {
 #pragma unroll
-        for (int s = 0; s < QF; ++s)
-          c = mfma_f32(Elem<T>::load(ks, (16 * j + col) * (D + KPAD) + s * 4 + grp), qf[s], c);
+        for (int s = 0; s < QF; ++s) {
+          const float a = Elem<T>::load(ks, (16 * j + col) * (D + KPAD) + s * 4 + grp);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+            if (live[qb]) st[qb][j] = mfma_f32(a, qf[qb][s], st[qb][j]);
+        }
       }
-      st[j] = c;
     }
 
-    // ---- online softmax (log2 domain), all state for this lane's query row.
+    // ---- online softmax (log2 domain), all state for this lane's query rows.
     // Raw scores are kept; the scale goes into the exponent's FMA
     // (sl2 > 0, so max(s * sl2) = sl2 * max(s)).  Tiles every row of the
-    // wave sees in full skip the mask.
-    if (kb0 + KT > kfull) {
+    // wave sees in full skip the mask.  v_exp_f32 is used directly: results
+    // below 2^-126 flush to 0, far under eps.
+    const bool full = kb0 + KT <= kfull;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      if (!live[qb]) continue;
+      if (!full) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kb0 + 16 * j + 4 * grp + i;
+            const bool ok = key < Lk && (!causal || key <= qp[qb]) && row_ok[qb];
+            st[qb][j][i] = ok ? st[qb][j][i] : -INFINITY;
+          }
+      }
+      float mb = -INFINITY;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kb0 + 16 * j + 4 * grp + i;
-          const bool ok = key < Lk && (!causal || key <= qp) && row_ok;
-          st[j][i] = ok ? st[j][i] : -INFINITY;
-        }
-    }
-    float mb = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) mb = fmaxf(mb, st[j][i]);
-    mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
-    mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-    const float mn = fmaxf(m_run, mb * sl2);
-    // v_exp_f32 directly (exp2 of the log2-domain score): results below
-    // 2^-126 flush to 0, far under eps; no libm range reduction per score.
-    float alpha, ps = 0.f;
-    if (kb0 + KT <= kfull) {  // every score finite: mn finite
-      alpha = __builtin_amdgcn_exp2f(m_run - mn);
+        for (int i = 0; i < 4; ++i) mb = fmaxf(mb, st[qb][j][i]);
+      mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+      mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+      const float mn = fmaxf(m_run[qb], mb * sl2);
+      float alpha, ps = 0.f;
       const float nmn = -mn;
+      if (full) {  // every score finite: mn finite
+        alpha = __builtin_amdgcn_exp2f(m_run[qb] - mn);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(st[j][i], sl2, nmn));
-          st[j][i] = p;
-          ps += p;
-        }
-    } else {  // rows with no visible key yet keep mn = -inf
-      alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
-      const float nmn = -mn;
+          for (int i = 0; i < 4; ++i) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(st[qb][j][i], sl2, nmn));
+            st[qb][j][i] = p;
+            ps += p;
+          }
+      } else {  // rows with no visible key yet keep mn = -inf
+        alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run[qb] - mn);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = (mn == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(fmaf(st[j][i], sl2, nmn));
-          st[j][i] = p;
-          ps += p;
-        }
-    }
-    l_run = fmaf(l_run, alpha, ps);
-    m_run = mn;
-    if (__any(alpha != 1.f)) {  // the running max of some row moved
+          for (int i = 0; i < 4; ++i) {
+            const float p =
+                (mn == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(fmaf(st[qb][j][i], sl2, nmn));
+            st[qb][j][i] = p;
+            ps += p;
+          }
+      }
+      l_run[qb] = fmaf(l_run[qb], alpha, ps);
+      m_run[qb] = mn;
+      if (__any(alpha != 1.f)) {  // the running max of some row moved
 #pragma unroll
-      for (int i = 0; i < DT; ++i) acc[i] *= alpha;
+        for (int i = 0; i < DT; ++i) acc[qb][i] *= alpha;
+      }
     }
 
     // ---- O^T += V^T P^T
@@ -616,19 +695,25 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
       const uint16_t* vt = reinterpret_cast<const uint16_t*>(vs);
 #pragma unroll
       for (int c2 = 0; c2 < 2; ++c2) {
-        uint4 pu;
-        pu.x = pack_bf16x2(st[2 * c2][0], st[2 * c2][1]);
-        pu.y = pack_bf16x2(st[2 * c2][2], st[2 * c2][3]);
-        pu.z = pack_bf16x2(st[2 * c2 + 1][0], st[2 * c2 + 1][1]);
-        pu.w = pack_bf16x2(st[2 * c2 + 1][2], st[2 * c2 + 1][3]);
-        const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, pu);
+        bf16x8_t pb[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          uint4 pu;
+          pu.x = pack_bf16x2(st[qb][2 * c2][0], st[qb][2 * c2][1]);
+          pu.y = pack_bf16x2(st[qb][2 * c2][2], st[qb][2 * c2][3]);
+          pu.z = pack_bf16x2(st[qb][2 * c2 + 1][0], st[qb][2 * c2 + 1][1]);
+          pu.w = pack_bf16x2(st[qb][2 * c2 + 1][2], st[qb][2 * c2 + 1][3]);
+          pb[qb] = __builtin_bit_cast(bf16x8_t, pu);
+        }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           const uint16_t* vr = vt + (dt * 16 + col) * (KT + VPAD);
           const uint2 lo = *reinterpret_cast<const uint2*>(vr + 32 * c2 + 4 * grp);
           const uint2 hi = *reinterpret_cast<const uint2*>(vr + 32 * c2 + 16 + 4 * grp);
-          const uint4 au = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          acc[dt] = mfma_bf16(__builtin_bit_cast(bf16x8_t, au), pb, acc[dt]);
+          const bf16x8_t a = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+            if (live[qb]) acc[qb][dt] = mfma_bf16(a, pb[qb], acc[qb][dt]);
         }
       }
     } else {
@@ -638,25 +723,32 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(
         for (int i = 0; i < 4; ++i) {
           const int key = 16 * j + 4 * grp + i;
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
-            acc[dt] = mfma_f32(Elem<T>::load(vs, key * (D + VPAD) + dt * 16 + col), st[j][i], acc[dt]);
+          for (int dt = 0; dt < DT; ++dt) {
+            const float a = Elem<T>::load(vs, key * (D + VPAD) + dt * 16 + col);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+              if (live[qb]) acc[qb][dt] = mfma_f32(a, st[qb][j][i], acc[qb][dt]);
+          }
         }
     }
     __syncthreads();
   }
 
-  float l_tot = l_run;
-  l_tot += __shfl_xor(l_tot, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
-  if (row_ok) {
-    const float inv = 1.f / fmaxf(l_tot, eps);
-    // out_tm: token-major [B, Lq, Hq, D] (the o_proj input); else [B, Hq, Lq, D]
-    T* orow = out + (out_tm ? (((int64_t)b * Lq + row) * Hq + hq) * D
-                            : (((int64_t)b * Hq + hq) * Lq + row) * D);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int qb = 0; qb < QB; ++qb) {
+    float l_tot = l_run[qb];
+    l_tot += __shfl_xor(l_tot, 16, 64);
+    l_tot += __shfl_xor(l_tot, 32, 64);
+    if (row_ok[qb]) {
+      const float inv = 1.f / fmaxf(l_tot, eps);
+      // out_tm: token-major [B, Lq, Hq, D] (the o_proj input); else [B, Hq, Lq, D]
+      T* orow = out + (out_tm ? (((int64_t)b * Lq + row[qb]) * Hq + hq) * D
+                              : (((int64_t)b * Hq + hq) * Lq + row[qb]) * D);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) Elem<T>::store(orow, dt * 16 + 4 * grp + i, acc[dt][i] * inv);
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Elem<T>::store(orow, dt * 16 + 4 * grp + i, acc[qb][dt][i] * inv);
+    }
   }
 }
 
@@ -798,15 +890,18 @@ int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v,
   }
   if constexpr (sizeof(TQ) == sizeof(TK) && sizeof(TK) == sizeof(TV)) {
     if (Lq > 1 && (D == 64 || D == 128)) {
-      dim3 grid((Lq + 63) / 64, Hq, B);
+      // bf16: two 16-row query blocks per wave (128 queries per workgroup)
+      constexpr int QB = sizeof(TQ) == 2 ? 2 : 1;
+      const int nqt = (Lq + 64 * QB - 1) / (64 * QB);
+      dim3 grid(prefill_grid(nqt, B, Hkv, Hq / Hkv));
       if (D == 64)
-        hipLaunchKernelGGL((attn_prefill_mfma<TQ, 64>), grid, dim3(256), 0, stream, (const TQ*)q,
-                           (const TQ*)k, (const TQ*)v, kv_bs, kv_hs, qpos, Hq, Hkv, Lq, Lk, causal,
-                           scale, eps, ex.out_tm, (TQ*)out);
+        hipLaunchKernelGGL((attn_prefill_mfma<TQ, 64, QB>), grid, dim3(256), 0, stream,
+                           (const TQ*)q, (const TQ*)k, (const TQ*)v, kv_bs, kv_hs, qpos, B, Hq,
+                           Hkv, Lq, Lk, causal, scale, eps, ex.out_tm, (TQ*)out);
       else
-        hipLaunchKernelGGL((attn_prefill_mfma<TQ, 128>), grid, dim3(256), 0, stream, (const TQ*)q,
-                           (const TQ*)k, (const TQ*)v, kv_bs, kv_hs, qpos, Hq, Hkv, Lq, Lk, causal,
-                           scale, eps, ex.out_tm, (TQ*)out);
+        hipLaunchKernelGGL((attn_prefill_mfma<TQ, 128, QB>), grid, dim3(256), 0, stream,
+                           (const TQ*)q, (const TQ*)k, (const TQ*)v, kv_bs, kv_hs, qpos, B, Hq,
+                           Hkv, Lq, Lk, causal, scale, eps, ex.out_tm, (TQ*)out);
       STRATA_HIP_CHECK(hipGetLastError());
       return STRATA_OK;
     }
