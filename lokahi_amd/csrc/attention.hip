@@ -200,12 +200,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         mb = fmaxf(mb, sc[jj]);
       }
       const float mn = fmaxf(m[g], mb);
+      // v_exp_f32 directly: exp2(-inf) = 0, results below 2^-126 flush to 0
       if (mn != -INFINITY) {
-        const float alpha = exp2f(m[g] - mn);
+        const float alpha = __builtin_amdgcn_exp2f(m[g] - mn);
         float ps = 0.f;
         float pj[J];
 #pragma unroll
-        for (int jj = 0; jj < J; ++jj) { pj[jj] = exp2f(sc[jj] - mn); ps += pj[jj]; }
+        for (int jj = 0; jj < J; ++jj) { pj[jj] = __builtin_amdgcn_exp2f(sc[jj] - mn); ps += pj[jj]; }
         s[g] = fmaf(s[g], alpha, ps);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       float ss = 0.f, oo = 0.f;
 #pragma unroll
       for (int w = 0; w < NS; ++w) {
-        const float f = ms[w].y > 0.f ? exp2f(ms[w].x - mx) : 0.f;
+        const float f = ms[w].y > 0.f ? __builtin_amdgcn_exp2f(ms[w].x - mx) : 0.f;
         ss = fmaf(ms[w].y, f, ss);
         oo = fmaf(ov[w], f, oo);
       }
@@ -315,8 +316,8 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict
     // it): with no key seen yet mb stays -inf and every weight below is 0.
     const float mb = fmaxf(mx, wave_max(my.y > 0.f ? my.x : -INFINITY));
     const float mref = mb == -INFINITY ? 0.f : mb;
-    const float alpha = mx == -INFINITY ? 0.f : exp2f(mx - mref);
-    const float w = my.y > 0.f ? exp2f(my.x - mref) : 0.f;  // 0 for splits past nsplit
+    const float alpha = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mx - mref);
+    const float w = my.y > 0.f ? __builtin_amdgcn_exp2f(my.x - mref) : 0.f;  // 0 for splits past nsplit
     ss = fmaf(ss, alpha, wave_sum(my.y * w));
     acc.x *= alpha; acc.y *= alpha; acc.z *= alpha; acc.w *= alpha;
 #pragma unroll
