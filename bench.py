@@ -55,7 +55,7 @@ def parse():
     p.add_argument("--gemv-iters", type=int, default=50)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
-    p.add_argument("--profile", choices=["gemv"], default=None)
+    p.add_argument("--profile", choices=["gemv", "prefill"], default=None)
     return p.parse_args()
 
 
@@ -153,6 +153,30 @@ def profile_gemv(iters):
         b.copy_(a)
     torch.cuda.synchronize()
     print(json.dumps({"profile": "gemv", "iters": iters, "copy_bytes_read": a.numel() * 4}))
+
+
+def profile_prefill(iters=3):
+    """Config 5's kernels alone (for rocprofv3 passes): the causal bf16
+    attention at 8192 tokens and the 8B gate projection at M = 8192 (weight
+    dequantize + library GEMM), each ``iters`` times."""
+    import torch
+    from lokahi_amd import ops
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(5)
+    L = 8192
+    q = torch.randn((1, 32, L, 128), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((1, 8, L, 128), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((1, 8, L, 128), generator=g, device=dev).to(torch.bfloat16)
+    for _ in range(iters):
+        ops.attention(q, k, v, causal=True)
+    x = torch.randn((L, 4096), generator=g, device=dev).to(torch.bfloat16)
+    w = ops.quantize(torch.randn((14336, 4096), generator=g, device=dev) * 0.02)
+    for _ in range(iters):
+        ops.linear(x, *w)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": "prefill", "iters": iters,
+                      "attention_flops": 4 * 32 * 128 * L * (L + 1) // 2,
+                      "gate_gemm_flops": 2 * L * 14336 * 4096}))
 
 
 def attention_decode():
@@ -359,6 +383,9 @@ def main():
     import torch
     if args.profile == "gemv":
         profile_gemv(args.gemv_iters)
+        return
+    if args.profile == "prefill":
+        profile_prefill()
         return
     from lokahi_amd.llama import LLAMA3_8B
 
