@@ -1,0 +1,53 @@
+"""BASELINE config 5 at full size (8192 tokens): parity by sampled rows and by
+properties that hold at any size (prefill row == decode over the same keys;
+library GEMM == fused-kernel GEMM)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import q4
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+from tests.gpu_util import rel_err, to_dev, to_np_f32
+from tests.test_gpu_attention import _c_decode
+
+pytestmark = pytest.mark.gpu
+TOL_BF16 = 2e-2
+TOL_F32 = 1e-3
+
+
+def test_config5_attention_8k_rows_match_oracle_and_decode(dev):
+    from lokahi_amd import ops
+    L, Hq, Hkv, D = 8192, 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(8192)
+    q = torch.randn((1, Hq, L, D), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((1, Hkv, L, D), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((1, Hkv, L, D), generator=g, device=dev).to(torch.bfloat16)
+    out = ops.attention(q, k, v, causal=True, q_block_size=512, k_block_size=512)
+    for row in (0, 63, 64, 1000, 4095, 8191):  # tile edges, the diagonal, the last row
+        qr = q[:, :, row:row + 1].contiguous()
+        kr, vr = k[:, :, :row + 1].contiguous(), v[:, :, :row + 1].contiguous()
+        dec = ops.attention(qr, kr, vr)  # decode kernel: query at position row
+        got = to_np_f32(out[:, :, row:row + 1])
+        assert rel_err(got, to_np_f32(dec)) < TOL_BF16, row
+        if row in (64, 4095, 8191):
+            kb = kr.cpu().view(torch.int16).numpy().view(np.uint16)
+            vb = vr.cpu().view(torch.int16).numpy().view(np.uint16)
+            ref = _c_decode(to_np_f32(qr), kb, vb)
+            assert rel_err(got, ref) < TOL_BF16, row
+
+
+def test_config5_gate_gemm_8k_library_and_fused_paths(dev, monkeypatch):
+    from lokahi_amd import ops
+    M, N, K = 8192, 14336, 4096
+    rng = np.random.default_rng(14336)
+    w, s, b = q4.quantize(rng.normal(0, 0.02, (N, K)).astype(np.float32), 64)
+    x = f32_to_bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
+    tw, ts, tb, tx = (to_dev(a, dev) for a in (w, s, b, x))
+    monkeypatch.setenv("STRATA_GEMM_LT_MIN_M", "256")
+    lib = ops.linear(tx, tw, ts, tb, out_dtype=torch.float32)
+    monkeypatch.setenv("STRATA_GEMM_LT_MIN_M", "0")
+    fused = ops.linear(tx, tw, ts, tb, out_dtype=torch.float32)
+    assert rel_err(to_np_f32(lib), to_np_f32(fused)) < TOL_F32
+    rows = np.array([0, 1, 255, 256, 4097, 8191])
+    ref = q4.quantized_matmul(bf16_bits_to_f32(x[rows]), w, s, b)
+    assert rel_err(to_np_f32(lib)[rows], ref) < TOL_BF16
