@@ -173,11 +173,16 @@ __device__ __forceinline__ void stage_x(const XT* __restrict__ x, int M, int K, 
 template <int MT, int XI>
 struct XStage {
   uint4 v[XI][4];
+  uint4 wn[XI][4];  // RMSNorm weights of the same items (NORM kernels)
 };
 
-template <int MT, int XI>
+// x items (and, for the RMSNorm prologue, the norm weights of the same
+// items) are loaded before the weight stream is issued: loads return in
+// order, so anything issued after the weights would wait for all of them.
+template <int MT, int XI, bool NORM = false>
 __device__ __forceinline__ void xstage_load(XStage<MT, XI>& st, const uint16_t* __restrict__ x,
-                                            int M, int K, int m0, int nv) {
+                                            int M, int K, int m0, int nv,
+                                            const uint16_t* __restrict__ norm_w = nullptr) {
 #pragma unroll
   for (int k = 0; k < XI; ++k) {
     const int idx = min((int)(threadIdx.x + k * blockDim.x), MT * nv - 1);
@@ -186,6 +191,11 @@ __device__ __forceinline__ void xstage_load(XStage<MT, XI>& st, const uint16_t* 
     const uint4* xr = reinterpret_cast<const uint4*>(x + (int64_t)m * K + (int64_t)i * 32);
 #pragma unroll
     for (int j = 0; j < 4; ++j) st.v[k][j] = xr[j];
+    if constexpr (NORM) {
+      const uint4* wr = reinterpret_cast<const uint4*>(norm_w) + i * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) st.wn[k][j] = wr[j];
+    }
   }
 }
 
@@ -228,7 +238,6 @@ __device__ __forceinline__ void xstage_norm(XStage<MT, XI>& st, int M, int K, in
                                             const NormArgs& na) {
   __shared__ float red[NW][MT];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint4 wn[XI][4];
   float ss[MT];
 #pragma unroll
   for (int mm = 0; mm < MT; ++mm) ss[mm] = 0.f;
@@ -236,10 +245,7 @@ __device__ __forceinline__ void xstage_norm(XStage<MT, XI>& st, int M, int K, in
   for (int k = 0; k < XI; ++k) {
     const int idx = threadIdx.x + k * blockDim.x;
     const int ic = min(idx, MT * nv - 1);
-    const int mm = ic / nv, i = ic - mm * nv;
-    const uint4* wr = reinterpret_cast<const uint4*>(na.w) + i * 4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) wn[k][j] = wr[j];
+    const int mm = ic / nv;
     const bool live = idx < MT * nv && m0 + mm < M;
     float sq = 0.f;
 #pragma unroll
@@ -281,7 +287,7 @@ __device__ __forceinline__ void xstage_norm(XStage<MT, XI>& st, int M, int K, in
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint32_t* u = reinterpret_cast<uint32_t*>(&st.v[k][j]);
-      const uint32_t wu[4] = {wn[k][j].x, wn[k][j].y, wn[k][j].z, wn[k][j].w};
+      const uint32_t wu[4] = {st.wn[k][j].x, st.wn[k][j].y, st.wn[k][j].z, st.wn[k][j].w};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const float lo = mul_rn(mul_rn(__uint_as_float(u[c] << 16), r), __uint_as_float(wu[c] << 16));
@@ -471,7 +477,7 @@ void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
 
   if constexpr (XI > 0) {
     XStage<MT, XI> st;
-    xstage_load<MT, XI>(st, reinterpret_cast<const uint16_t*>(x), M, K, m0, nv);
+    xstage_load<MT, XI, NORM>(st, reinterpret_cast<const uint16_t*>(x), M, K, m0, nv, na.w);
     issue(0);
     prefetch_rope();
     __builtin_amdgcn_sched_barrier(0);
