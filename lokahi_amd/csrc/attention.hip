@@ -109,14 +109,19 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const TQ* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
     int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Hkv, int Lk,
     const int* __restrict__ dlen, int causal, int chunk, int nsplit, float scale, float eps,
-    float* __restrict__ part, TQ* __restrict__ out) {
+    float* __restrict__ part, TQ* __restrict__ out, int gfull) {
   constexpr int EPL = 16 / sizeof(TK);          // key elements per lane
   constexpr int LPK = D / EPL;                  // lanes per key
   constexpr int KPW = 64 / LPK;                 // keys per wave step
   constexpr int J = 4;                          // keys per stream per step
   static_assert(LPK <= 64 && 64 % LPK == 0, "unsupported head dim");
 
-  const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
+  // blockIdx.y = (kv head, slice): the workgroup serves G of the gfull query
+  // heads of its KV head, hq0 .. hq0 + G - 1.
+  const int split = blockIdx.x, b = blockIdx.z;
+  const int hslices = gfull / G;
+  const int hkv = blockIdx.y / hslices;
+  const int hq0 = hkv * gfull + (blockIdx.y - hkv * hslices) * G;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / LPK, part_idx = lane % LPK;
   const int e0 = part_idx * EPL;
@@ -161,7 +166,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   float qv[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; ++g)
-    load_elems<TQ, EPL>(q + ((int64_t)b * Hq + hkv * G + g) * D + e0, qv[g]);
+    load_elems<TQ, EPL>(q + ((int64_t)b * Hq + hq0 + g) * D + e0, qv[g]);
 
   float m[G], s[G], o[G][EPL];
 #pragma unroll
@@ -267,7 +272,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         ss = fmaf(ms[w].y, f, ss);
         oo = fmaf(ov[w], f, oo);
       }
-      const int hq = hkv * G + g0 + gl;
+      const int hq = hq0 + g0 + gl;
       if (nsplit == 1) {
         Elem<TQ>::store(out, ((int64_t)b * Hq + hq) * D + d, oo / fmaxf(ss, eps));
       } else {
@@ -844,12 +849,23 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
       part = reinterpret_cast<float*>(p);
     }
   }
-  dim3 grid(nsplit, Hkv, B);
+  // Query heads per workgroup: the whole group reads K/V once; while the grid
+  // has fewer workgroups than CUs (short contexts) the group is halved, so
+  // each wave's chain is shorter (measured at 64-1024 keys: 1-1.6 us faster;
+  // at 2k+ keys the full group is as fast or faster).
+  // STRATA_ATTN_HEADS_PER_WG picks a divisor of the group instead.
+  int HG = G;
+  while (HG % 2 == 0 && (int64_t)nsplit * B * Hkv * (G / HG) < ctx->num_cus) HG /= 2;
+  if (const char* e = getenv("STRATA_ATTN_HEADS_PER_WG")) {
+    const int h = atoi(e);
+    if (h > 0 && G % h == 0 && (h == 1 || h == 2 || h == 3 || h == 4 || h == 6 || h == 8)) HG = h;
+  }
+  dim3 grid(nsplit, Hkv * (G / HG), B);
 #define STRATA_DEC(GV)                                                                        \
-  if (G == GV)                                                                                \
+  if (HG == GV)                                                                               \
     hipLaunchKernelGGL((attn_decode_kernel<TQ, TK, TV, D, GV>), grid, dim3(256), 0, stream,   \
                        (const TQ*)q, (const TK*)k, (const TV*)v, kv_bs, kv_hs, qpos, Hq, Hkv, \
-                       Lk, ex.dlen, causal, chunk, nsplit, scale, eps, part, (TQ*)out);
+                       Lk, ex.dlen, causal, chunk, nsplit, scale, eps, part, (TQ*)out, G);
   STRATA_DEC(1) else STRATA_DEC(2) else STRATA_DEC(3) else STRATA_DEC(4) else STRATA_DEC(6) else
   STRATA_DEC(8) else
     return strata_set_error(STRATA_ENOTSUP, "decode attention: group size %d not in {1,2,3,4,6,8}",
