@@ -106,12 +106,30 @@ int lt_init(strata_ctx* ctx) {
   return STRATA_OK;
 }
 
-int lt_plan(GemmLt* lt, int M, int N, int K, int y_dtype, Plan** out) {
+void plan_release(Plan& p) {
+  if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
+  if (p.b) hipblasLtMatrixLayoutDestroy(p.b);
+  if (p.c) hipblasLtMatrixLayoutDestroy(p.c);
+  if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+}
+
+// Plans are cached per (M, N, K, output dtype).  Prefill M is the prompt
+// length, so the cache is bounded: past kMaxPlans entries it is emptied
+// (the caller's stream is synchronized first: queued GEMMs may still use a
+// plan's descriptors).
+constexpr size_t kMaxPlans = 256;
+
+int lt_plan(GemmLt* lt, int M, int N, int K, int y_dtype, void* stream, Plan** out) {
   auto key = std::make_tuple(M, N, K, y_dtype);
   auto it = lt->plans.find(key);
   if (it != lt->plans.end()) {
     *out = &it->second;
     return STRATA_OK;
+  }
+  if (lt->plans.size() >= kMaxPlans) {
+    STRATA_HIP_CHECK(hipStreamSynchronize(as_stream(stream)));
+    for (auto& kv : lt->plans) plan_release(kv.second);
+    lt->plans.clear();
   }
   Plan p;
   const hipDataType yt = y_dtype == STRATA_F32 ? HIP_R_32F : HIP_R_16BF;
@@ -156,13 +174,7 @@ int strata_q4_dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_
 void strata_gemm_lt_destroy(strata_ctx* ctx) {
   GemmLt* lt = ctx->lt;
   if (!lt) return;
-  for (auto& kv : lt->plans) {
-    Plan& p = kv.second;
-    if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
-    if (p.b) hipblasLtMatrixLayoutDestroy(p.b);
-    if (p.c) hipblasLtMatrixLayoutDestroy(p.c);
-    if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
-  }
+  for (auto& kv : lt->plans) plan_release(kv.second);
   if (lt->wdq) (void)hipFree(lt->wdq);
   if (lt->workspace) (void)hipFree(lt->workspace);
   if (lt->handle) hipblasLtDestroy(lt->handle);
@@ -180,7 +192,7 @@ int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t*
   if (rc) return rc;
   GemmLt* lt = ctx->lt;
   Plan* p = nullptr;
-  rc = lt_plan(lt, M, N, K, y_dtype, &p);
+  rc = lt_plan(lt, M, N, K, y_dtype, stream, &p);
   if (rc) return rc;
   if (!p->ok)  // no library kernel for this shape: the fused-dequant kernel covers it
     return strata_q4_gemm_launch(x, M, K, w, s, b, N, y, y_dtype, stream);
