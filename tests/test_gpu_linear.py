@@ -153,3 +153,20 @@ def test_quantizer_is_bit_exact_with_oracle(dev):
     assert np.array_equal(pw.cpu().view(torch.int32).numpy().view(np.uint32), ew)
     assert np.array_equal(sc.cpu().view(torch.int16).numpy().view(np.uint16), es)
     assert np.array_equal(bi.cpu().view(torch.int16).numpy().view(np.uint16), eb)
+
+
+def test_gemm_library_plan_cache_survives_many_prompt_lengths(dev, monkeypatch):
+    """Prefill M is the prompt length: more distinct lengths than the plan
+    cache holds (256) must keep giving correct results across the eviction."""
+    from lokahi_amd import ops
+    monkeypatch.setenv("STRATA_GEMM_LT_MIN_M", "1")
+    rng = np.random.default_rng(260)
+    N, K = 64, 128
+    w, s, b, x = _problem(rng, N, K, 600)
+    tw, ts, tb, tx = (to_dev(a, dev) for a in (w, s, b, x))
+    wq = round_bf16(q4.dequantize(w, s, b, 64).astype(np.float32)).astype(np.float64)
+    for M in range(300, 560):
+        y = ops.linear(tx[:M], tw, ts, tb, out_dtype=torch.float32)
+        if M in (300, 301, 555, 559):
+            ref = bf16_bits_to_f32(x[:M]).astype(np.float64) @ wq.T
+            assert rel_err(to_np_f32(y), ref) < TOL_F32, M
