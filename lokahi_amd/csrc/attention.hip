@@ -8,15 +8,17 @@
 //
 // Three kernels:
 //   * attn_decode_kernel : Lq == 1.  Split-K over the key axis; each workgroup
-//     streams one key chunk of one KV head for all G = Hq/Hkv query heads
-//     (K/V read once per group), keeps per-16-lane online-softmax state in
-//     registers, merges its lanes through LDS and writes (m, s, o[D]) partials;
+//     streams one key chunk of one KV head for its query heads (the whole
+//     group G = Hq/Hkv, K/V read once, or half of it when the grid would not
+//     fill the GPU), keeps per-16-lane online-softmax state in registers,
+//     merges its lanes through LDS and writes (m, s, o[D]) partials;
 //     attn_decode_merge combines the chunks.
 //   * attn_prefill_mfma : Lq > 1, D in {64, 128}, q/k/v of one dtype.
 //     Flash-style: 64-key K / V^T tiles staged in LDS, S^T = K Q^T and
 //     O^T += V^T P^T on MFMA (bf16 16x16x32, or f32 16x16x4 for fp32 inputs),
-//     so every lane owns one query row and all softmax state is in-lane.
-//     Key blocks past the causal limit of the 64-query tile are skipped.
+//     so every lane owns one query row (of each of the wave's 16-row query
+//     blocks) and all softmax state is in-lane.  Key blocks past the causal
+//     limit of the workgroup's query tile are skipped.
 //   * attn_generic : any other shape (e.g. tiny head dims), one wave per query.
 #include <algorithm>
 #include <cstdlib>

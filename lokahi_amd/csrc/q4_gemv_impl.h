@@ -791,10 +791,10 @@ int dispatch_q4(strata_ctx* ctx, const void* x, int M, int K, const Q4Batch& bat
   else if (g.mt == 2) ok = launch_q4_u<4, 2, 2, EPI, NORM, XT, YT>(g, x, M, K, batch, na, lds, stream);
   else if (g.nw == 4 && g.r == 2) ok = launch_q4_u<4, 2, 1, EPI, NORM, XT, YT>(g, x, M, K, batch, na, lds, stream);
   else if constexpr (!kPair) {
-    if (g.nw == 4 && g.r == 4) ok = launch_q4_u<4, 4, 1, EPI, NORM, XT, YT>(g, x, M, K, batch, na, lds, stream);
-    else if (g.nw == 4 && g.r == 1) ok = launch_q4_u<4, 1, 1, EPI, NORM, XT, YT>(g, x, M, K, batch, na, lds, stream);
+    // (4 rows per wave, or 8 waves x 2 rows, spill registers at long rows and
+    // never won a measurement: not built)
+    if (g.nw == 4 && g.r == 1) ok = launch_q4_u<4, 1, 1, EPI, NORM, XT, YT>(g, x, M, K, batch, na, lds, stream);
     else if (g.nw == 8 && g.r == 1) ok = launch_q4_u<8, 1, 1, EPI, NORM, XT, YT>(g, x, M, K, batch, na, lds, stream);
-    else if (g.nw == 8 && g.r == 2) ok = launch_q4_u<8, 2, 1, EPI, NORM, XT, YT>(g, x, M, K, batch, na, lds, stream);
   }
   if (!ok)
     return strata_set_error(STRATA_EINVAL, "q4 GEMV: no kernel for geometry nw=%d r=%d u=%d mt=%d",
