@@ -5,25 +5,73 @@ Availability is fail-closed like ``MetalBackend`` (``metal_backend.py:74-163``):
 the backend is available only if ``libstrata_hip.so`` loads, a context binds to
 a gfx950 device, and the library's self-test envelope reports
 ``dispatch_success`` with ``numerical_max_error`` under its threshold.
+
+With ``probe_path`` (or ``STRATA_HIP_PROBE``) the evidence comes, as in
+``MetalBackend``, from a native executable (``lokahi_amd/_lib/strata-hip-probe``)
+run as a child process: one JSON envelope on stdout (schema_version 1,
+backend "hip", dispatch_success, device_name, operation, dtype,
+numerical_max_error, timing.average_dispatch_wall_time_ms, failure_reason)
+and a zero exit status.
 """
 from __future__ import annotations
 
 import json
+import os
+import subprocess
+from pathlib import Path
 from typing import Any, Optional
 
 from .base import (Backend, BackendError, ComputeUnit, InferencePhase, OperationKind,
                    RuntimeCapabilities)
 
 
+DEFAULT_PROBE = Path(__file__).resolve().parents[1] / "_lib" / "strata-hip-probe"
+
+
 class HipBackend(Backend):
     name = "hip"
 
-    def __init__(self):
+    def __init__(self, probe_path: Optional[str] = None, timeout_seconds: float = 60.0,
+                 maximum_error: float = 1e-4):
         self._probe: Optional[dict] = None
         self._probe_error: Optional[str] = None
+        self._probe_path = probe_path or os.environ.get("STRATA_HIP_PROBE")
+        self._timeout = timeout_seconds
+        self._maximum_error = maximum_error
+
+    def _probe_executable(self) -> dict:
+        """Evidence from the native probe (``metal_backend.py:74-163`` contract)."""
+        path = Path(self._probe_path).expanduser()
+        if not path.is_file() or not os.access(path, os.X_OK):
+            raise BackendError("native HIP probe is missing or not executable")
+        try:
+            done = subprocess.run([str(path)], capture_output=True, check=False, text=True,
+                                  timeout=self._timeout)
+        except (OSError, subprocess.SubprocessError) as exc:
+            raise BackendError(f"native HIP probe failed to execute: {exc}")
+        try:
+            env = json.loads(done.stdout)
+            if not isinstance(env, dict):
+                raise ValueError("root JSON value is not an object")
+        except (json.JSONDecodeError, ValueError) as exc:
+            raise BackendError(f"native HIP probe returned invalid JSON: {exc}")
+        if env.get("schema_version") != 1 or env.get("backend") != "hip":
+            raise BackendError("native HIP probe returned an unsupported evidence envelope")
+        if done.returncode != 0 or env.get("dispatch_success") is not True:
+            raise BackendError(env.get("failure_reason")
+                               or f"native HIP probe exited with status {done.returncode}")
+        err = env.get("numerical_max_error")
+        if not isinstance(err, (int, float)) or not 0 <= err <= self._maximum_error:
+            raise BackendError("native HIP evidence did not satisfy the capability contract")
+        return env
 
     def probe(self) -> dict:
         """Run (once) and return the self-test evidence envelope."""
+        if self._probe is None and self._probe_error is None and self._probe_path:
+            try:
+                self._probe = self._probe_executable()
+            except BackendError as exc:  # fail closed
+                self._probe_error = str(exc)
         if self._probe is None and self._probe_error is None:
             try:
                 import torch

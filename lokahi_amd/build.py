@@ -16,6 +16,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OUT_DIR = PKG / "_lib"
 LIB = OUT_DIR / "libstrata_hip.so"
+PROBE_SRC = PKG / "probe" / "strata_hip_probe.cpp"
+PROBE = OUT_DIR / "strata-hip-probe"  # native evidence-lane executable
 INCLUDE = PKG.parent / "include"
 
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
@@ -60,8 +62,15 @@ def build(verbose: bool = False) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    tmp = PROBE.with_suffix(".tmp")
+    cmd = [HIPCC, *COMMON, "-x", "hip", str(PROBE_SRC), "-o", str(tmp), f"-L{OUT_DIR}",
+           "-lstrata_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"probe build failed:\n{r.stderr}")
+    os.replace(tmp, PROBE)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {PROBE.name}")
     return LIB
 
 
