@@ -239,17 +239,18 @@ def prefill_8b():
                           "frac_mfma_bf16": round(aflops / aus / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}}
 
 
-def run_decode(cfg, prompt_len, new_tokens, seed):
-    """Prefill `prompt_len` uniform-random ids, then time `new_tokens` greedy
-    tokens on the native engine (warm pass first, so the step graphs exist)."""
+def run_decode(cfg, prompt_len, new_tokens, seed, batch=1):
+    """Prefill `prompt_len` uniform-random ids per row, then time `new_tokens`
+    greedy tokens per row on the native engine (warm pass first, so the step
+    graphs exist)."""
     import torch
     from lokahi_amd.llama import DecoderEngine, HipLlamaForCausalLM, random_weights
     weights = random_weights(cfg, seed=seed)
     model = HipLlamaForCausalLM(cfg, weights)
-    cache = model.new_cache(1, prompt_len + new_tokens + 8)
-    engine = DecoderEngine(model, cache, max_batch=1, max_tokens=prompt_len)
+    cache = model.new_cache(batch, prompt_len + new_tokens + 8)
+    engine = DecoderEngine(model, cache, max_batch=batch, max_tokens=batch * prompt_len)
     gen = torch.Generator().manual_seed(seed)
-    prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=gen)
+    prompt = torch.randint(0, cfg.vocab_size, (batch, prompt_len), generator=gen)
     times = []
     for rep in range(2):  # rep 0 warms up (captures the per-bucket step graphs)
         cache.clear()
@@ -275,6 +276,18 @@ def decode_bytes(cfg, ctx_avg):
     q4 = lin // 2 + 4 * (lin // 64)
     kv = 2 * 2 * cfg.num_key_value_heads * cfg.head_dim * ctx_avg
     return cfg.num_hidden_layers * (q4 + kv) + cfg.vocab_size * cfg.hidden_size * 2
+
+
+def decode_batch8():
+    """Serving view (not a BASELINE config): the 8B shape decoding 8 sequences
+    at once, 512-token prompts, 32 timed tokens per sequence; aggregate tok/s.
+    The q4 linears then run the batched GEMV (8 rows share each weight read)."""
+    from lokahi_amd.llama import LLAMA3_8B
+    B, P, T = 8, 512, 33
+    prefill_s, decode_s, _ = run_decode(LLAMA3_8B, P, T, seed=3, batch=B)
+    return {"batch": B, "prompt": P, "new_tokens_per_row": T,
+            "decode_tok_s": round(B * T / decode_s, 1),
+            "ms_per_step": round(1e3 * decode_s / T, 3), "prefill_s": round(prefill_s, 3)}
 
 
 def e2e_3b():
