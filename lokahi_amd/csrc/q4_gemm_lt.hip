@@ -133,25 +133,34 @@ int lt_plan(GemmLt* lt, int M, int N, int K, int y_dtype, void* stream, Plan** o
   }
   Plan p;
   const hipDataType yt = y_dtype == STRATA_F32 ? HIP_R_32F : HIP_R_16BF;
-  LT_CHECK(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
   const int32_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
-  LT_CHECK(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT)));
-  LT_CHECK(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN)));
-  LT_CHECK(hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, K, N, K));
-  LT_CHECK(hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, K, M, K));
-  LT_CHECK(hipblasLtMatrixLayoutCreate(&p.c, yt, N, M, N));
-  hipblasLtMatmulPreference_t pref;
-  LT_CHECK(hipblasLtMatmulPreferenceCreate(&pref));
   const uint64_t ws = kLtWorkspace;
-  LT_CHECK(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
-                                                 &ws, sizeof(ws)));
+  hipblasLtMatmulPreference_t pref = nullptr;
   hipblasLtMatmulHeuristicResult_t heur[1];
   int found = 0;
-  hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(lt->handle, p.desc, p.a, p.b, p.c, p.c,
-                                                       pref, 1, heur, &found);
-  hipblasLtMatmulPreferenceDestroy(pref);
-  p.ok = st == HIPBLAS_STATUS_SUCCESS && found > 0 && heur[0].workspaceSize <= kLtWorkspace;
-  if (p.ok) p.algo = heur[0].algo;
+  // any failure releases what was created and leaves the shape unplanned
+  bool built =
+      hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT)) ==
+          HIPBLAS_STATUS_SUCCESS &&
+      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN)) ==
+          HIPBLAS_STATUS_SUCCESS &&
+      hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, K, N, K) == HIPBLAS_STATUS_SUCCESS &&
+      hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, K, M, K) == HIPBLAS_STATUS_SUCCESS &&
+      hipblasLtMatrixLayoutCreate(&p.c, yt, N, M, N) == HIPBLAS_STATUS_SUCCESS &&
+      hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+      hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                            sizeof(ws)) == HIPBLAS_STATUS_SUCCESS;
+  built = built && hipblasLtMatmulAlgoGetHeuristic(lt->handle, p.desc, p.a, p.b, p.c, p.c, pref,
+                                                   1, heur, &found) == HIPBLAS_STATUS_SUCCESS;
+  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  p.ok = built && found > 0 && heur[0].workspaceSize <= kLtWorkspace;
+  if (p.ok) {
+    p.algo = heur[0].algo;
+  } else {
+    plan_release(p);  // the shape falls back to the fused kernel
+    p = Plan{};
+  }
   auto ins = lt->plans.emplace(key, p);
   *out = &ins.first->second;
   return STRATA_OK;
@@ -186,7 +195,7 @@ int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t*
                    const uint16_t* s, const uint16_t* b, int N, void* y, int y_dtype,
                    void* stream) {
   const int min_rows = lt_min_rows();
-  if (min_rows <= 0 || M < min_rows)
+  if (min_rows <= 0 || M < min_rows || !aligned16(y))
     return strata_q4_gemm_launch(x, M, K, w, s, b, N, y, y_dtype, stream);
   int rc = lt_init(ctx);
   if (rc) return rc;
@@ -206,9 +215,10 @@ int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t*
       lt->wdq = nullptr;
       lt->wdq_bytes = 0;
     }
-    if (hipMalloc(&lt->wdq, need) != hipSuccess) {
+    if (hipMalloc(&lt->wdq, need) != hipSuccess) {  // no room for the tile: fused kernel
       lt->wdq = nullptr;
-      return strata_set_error(STRATA_ENOMEM, "bf16 weight tile of %zu bytes failed", need);
+      (void)hipGetLastError();
+      return strata_q4_gemm_launch(x, M, K, w, s, b, N, y, y_dtype, stream);
     }
     lt->wdq_bytes = need;
   }
