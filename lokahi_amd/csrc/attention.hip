@@ -430,8 +430,12 @@ void attn_prefill_mfma(
   // K tile: [KT][D + KPAD]; V tile: bf16 -> transposed [D][KT + VPAD], f32 -> [KT][D + VPAD]
   constexpr int K_ELEMS = KT * (D + KPAD);
   constexpr int V_ELEMS = kBF16 ? D * (KT + VPAD) : KT * (D + VPAD);
-  __shared__ __attribute__((aligned(16))) T ks[K_ELEMS];
-  __shared__ __attribute__((aligned(16))) T vs[V_ELEMS];
+  // bf16: two LDS stages (2 x 34.8 KB; gfx950 allows 160 KB per workgroup)
+  // so tile t+1 is staged while other waves still compute on tile t, one
+  // barrier per tile.  fp32 tiles are twice as large: one stage.
+  constexpr int NBUF = kBF16 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) T ks_buf[NBUF][K_ELEMS];
+  __shared__ __attribute__((aligned(16))) T vs_buf[NBUF][V_ELEMS];
   __shared__ int s_kmax;
 
   const int G = Hq / Hkv;
@@ -569,19 +573,18 @@ void attn_prefill_mfma(
       }
     }
   };
-  if (kmax > 0) fetch(0);
-  for (int kb0 = 0; kb0 < kmax; kb0 += KT) {
-    // ---- stage K (row-major, padded) and V (bf16: transposed) tiles
+  // ---- stage K (row-major, padded) and V (bf16: transposed) tiles
+  auto stage = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < NCH; ++u) {
       const int c = threadIdx.x + 256 * u;
       int t, d0;
       tile_slot(c, t, d0);
-      *reinterpret_cast<uint4*>(&ks[t * (D + KPAD) + d0]) = kreg[u];
-      if constexpr (!kBF16) *reinterpret_cast<uint4*>(&vs[t * (D + VPAD) + d0]) = vreg[u];
+      *reinterpret_cast<uint4*>(&ks_buf[buf][t * (D + KPAD) + d0]) = kreg[u];
+      if constexpr (!kBF16) *reinterpret_cast<uint4*>(&vs_buf[buf][t * (D + VPAD) + d0]) = vreg[u];
     }
     if constexpr (kBF16) {
-      uint16_t* vt = reinterpret_cast<uint16_t*>(vs);
+      uint16_t* vt = reinterpret_cast<uint16_t*>(vs_buf[buf]);
 #pragma unroll
       for (int u = 0; u < NVB; ++u) {
         const int blk = threadIdx.x + 256 * u;
@@ -599,8 +602,18 @@ void attn_prefill_mfma(
           *reinterpret_cast<uint2*>(&vt[(4 * dg + j) * (KT + VPAD) + 4 * kg]) = o[j];
       }
     }
-    __syncthreads();
-    if (kb0 + KT < kmax) fetch(kb0 + KT);
+  };
+  if (kmax > 0) {
+    fetch(0);
+    stage(0);
+  }
+  __syncthreads();
+  for (int kb0 = 0, it = 0; kb0 < kmax; kb0 += KT, ++it) {
+    const int cur = NBUF == 2 ? (it & 1) : 0;
+    const T* ks = ks_buf[cur];
+    const T* vs = vs_buf[cur];
+    const bool more = kb0 + KT < kmax;
+    if (more) fetch(kb0 + KT);
     // Query blocks of this wave that see any key of the tile (causal: the
     // wave's later blocks may, its earlier ones may not, near the diagonal).
     bool live[QB];
@@ -739,7 +752,16 @@ void attn_prefill_mfma(
           }
         }
     }
-    __syncthreads();
+    if constexpr (NBUF == 2) {
+      if (more) stage(cur ^ 1);  // the other buffer: last read before the previous barrier
+      __syncthreads();
+    } else {
+      __syncthreads();  // every wave is done with the single buffer
+      if (more) {
+        stage(0);
+        __syncthreads();
+      }
+    }
   }
 
 #pragma unroll
