@@ -843,7 +843,9 @@ constexpr int kLongSplitKeys = 2048;
 void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
   int min_chunk = Lcap >= kLongSplitKeys ? 128 : 64;
   if (const char* e = getenv("STRATA_ATTN_MIN_CHUNK")) min_chunk = std::max(64, atoi(e));
-  int want = (num_cus * 4 + B * Hkv - 1) / (B * Hkv);
+  int per_cu = 4;
+  if (const char* e = getenv("STRATA_ATTN_SPLITS_PER_CU")) per_cu = std::max(1, atoi(e));
+  int want = (num_cus * per_cu + B * Hkv - 1) / (B * Hkv);
   if (want > kMaxDecodeSplits) want = kMaxDecodeSplits;
   int nsplit = (Lcap + min_chunk - 1) / min_chunk;
   if (nsplit > want) nsplit = want;

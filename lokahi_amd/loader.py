@@ -32,6 +32,7 @@ from __future__ import annotations
 
 import json
 import struct
+import warnings
 from pathlib import Path
 from typing import Dict, Iterable, List, Optional, Tuple
 
@@ -211,14 +212,19 @@ def checkpoint_names(cfg: LlamaConfig, *, quantized_embed: bool, head: str) -> L
 def load_mlx_llama(model_dir, device: int = 0) -> HipLlamaForCausalLM:
     """Load an MLX 4-bit Llama checkpoint directory (``config.json`` +
     safetensors) into a ``HipLlamaForCausalLM`` on ``cuda:device``."""
+    model_dir = Path(model_dir)
+    raw = json.loads((model_dir / "config.json").read_text())
+    cfg = config_from_dict(raw)
+    return build_llama(cfg, _Tensors(SafeTensorReader(p) for p in _files(model_dir)), device)
+
+
+def build_llama(cfg: LlamaConfig, t, device: int = 0) -> HipLlamaForCausalLM:
+    """Device weights from a tensor source ``t`` (``name in t``;
+    ``t.get(name, dtype, shape)`` -> ndarray) holding MLX checkpoint names."""
     import torch
 
     from . import ops
 
-    model_dir = Path(model_dir)
-    raw = json.loads((model_dir / "config.json").read_text())
-    cfg = config_from_dict(raw)
-    t = _Tensors(SafeTensorReader(p) for p in _files(model_dir))
     dev = torch.device("cuda", device)
     hs, fs, g = cfg.hidden_size, cfg.intermediate_size, cfg.group_size
     hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
@@ -227,11 +233,14 @@ def load_mlx_llama(model_dir, device: int = 0) -> HipLlamaForCausalLM:
             "down_proj": (hs, fs)}
 
     def up(a: np.ndarray) -> "torch.Tensor":
-        if a.dtype == np.uint16:
-            return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(dev)
-        if a.dtype == np.uint32:
-            return torch.from_numpy(a.view(np.int32)).view(torch.uint32).to(dev)
-        return torch.from_numpy(a).to(dev)
+        # read-only (mapped) host arrays are copied to the device at once
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore", UserWarning)
+            if a.dtype == np.uint16:
+                return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(dev)
+            if a.dtype == np.uint32:
+                return torch.from_numpy(a.view(np.int32)).view(torch.uint32).to(dev)
+            return torch.from_numpy(a).to(dev)
 
     def q4(prefix: str, n: int, k: int) -> Tuple["torch.Tensor", "torch.Tensor", "torch.Tensor"]:
         if prefix + ".scales" not in t:
