@@ -45,6 +45,7 @@ struct strata_decoder {
   float* part;            // split-K partials for graph-mode decode attention
   int part_splits;
   float2* rope_table;     // (cos, sin) [Lmax][head_dim/2], built once at creation
+  float2* rope_cur;       // (cos, sin) [head_dim/2] of the position counters[1]
   void* amax;             // argmax partials [max_batch * kArgmaxBlocks * 8 B]
   hipStream_t stream;     // the decoder's own stream (graph capture / replay)
   // Captured decode steps, one per key-capacity bucket: a step at key count
@@ -119,7 +120,7 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
       GemvEpilogue eq{2, D, Hq, Hkv, kv->Lmax, graph_mode ? 0 : pos0,
                       graph_mode ? d->counters + 1 : nullptr, c.rope_theta,
                       (uint16_t*)d->qr, (uint16_t*)kc, (uint16_t*)vc, Lw.input_norm,
-                      c.rms_norm_eps, d->rope_table};
+                      c.rms_norm_eps, d->rope_table, graph_mode ? d->rope_cur : nullptr};
       RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, qkv, 3, eq, stream));
       AttnExtra ex;
       ex.part = d->part;
@@ -272,6 +273,7 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
       {reinterpret_cast<void**>(&d->counters), 16},
       {&d->amax, (size_t)max_batch * kArgmaxBlocks * 8},
       {reinterpret_cast<void**>(&d->rope_table), (size_t)kv->Lmax * (c.head_dim / 2) * 8},
+      {reinterpret_cast<void**>(&d->rope_cur), (size_t)(c.head_dim / 2) * 8},
   };
   for (auto& b : bufs)
     if (!rc) rc = alloc(b.p, b.bytes);
@@ -298,7 +300,7 @@ int strata_decoder_destroy(strata_decoder* d) {
   for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
   void* ptrs[] = {d->h, d->xn, d->q, d->k, d->v, d->qr, d->attn, d->o, d->gate, d->up, d->act,
                   d->delta, d->hn, d->logits, d->ids, d->counters, d->part, d->amax,
-                  d->rope_table};
+                  d->rope_table, d->rope_cur};
   for (void* p : ptrs)
     if (p) hipFree(p);
   if (d->stream) hipStreamDestroy(d->stream);
@@ -361,13 +363,15 @@ int strata_decoder_generate(strata_decoder* d, const int32_t* prompt, int B, int
   // at position pos0+L against pos0+L+1 keys.
   const int init[4] = {0, pos0 + L - 1, pos0 + L, 0};
   STRATA_HIP_CHECK(hipMemcpyAsync(d->counters, init, sizeof(init), hipMemcpyHostToDevice, s));
-  RC(strata_decode_advance_launch(d->ids, B, out_tokens, max_new, d->counters, s));
+  RC(strata_decode_advance_launch(d->ids, B, out_tokens, max_new, d->counters, d->rope_table,
+                                  d->kv->Lmax, c.head_dim / 2, d->rope_cur, s));
 
   auto decode_step = [&](hipStream_t st, int key_cap) -> int {
     RC(strata_embed_launch(d->embed, c.vocab_size, c.hidden_size, d->ids, B, d->h, st));
     RC(forward_layers(d, B, 1, -1, st, key_cap));
     RC(strata_argmax_launch(d->logits, B, c.vocab_size, temperature, d->ids, d->amax, st));
-    RC(strata_decode_advance_launch(d->ids, B, out_tokens, max_new, d->counters, st));
+    RC(strata_decode_advance_launch(d->ids, B, out_tokens, max_new, d->counters, d->rope_table,
+                                    d->kv->Lmax, c.head_dim / 2, d->rope_cur, st));
     return STRATA_OK;
   };
   if (max_new > 1) {

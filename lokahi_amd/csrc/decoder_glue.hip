@@ -316,12 +316,19 @@ int strata_quantize_launch(const void* src, int dtype, int64_t N, int64_t K, int
 
 namespace {
 // End of a graph-replayed decode step: record the token chosen for each batch
-// row, and advance the device counters {step, position, key count}.
+// row, advance the device counters {step, position, key count}, and stage
+// the RoPE (cos, sin) row of the new position for the next step's q/k/v
+// epilogue (a position past the table is never used: nothing is staged).
 __global__ void decode_advance_kernel(const int32_t* __restrict__ ids, int B,
                                       int32_t* __restrict__ out, int out_stride,
-                                      int* __restrict__ counters) {
+                                      int* __restrict__ counters,
+                                      const float2* __restrict__ rope_table, int lmax, int half,
+                                      float2* __restrict__ rope_cur) {
   const int step = counters[0];
+  const int pos = counters[1] + 1;
   for (int b = threadIdx.x; b < B; b += blockDim.x) out[(int64_t)b * out_stride + step] = ids[b];
+  if (rope_cur && pos >= 0 && pos < lmax)
+    for (int t = threadIdx.x; t < half; t += blockDim.x) rope_cur[t] = rope_table[(int64_t)pos * half + t];
   __syncthreads();
   if (threadIdx.x == 0) {
     counters[0] = step + 1;
@@ -332,9 +339,10 @@ __global__ void decode_advance_kernel(const int32_t* __restrict__ ids, int B,
 }  // namespace
 
 int strata_decode_advance_launch(const int32_t* ids, int B, int32_t* out_tokens, int out_stride,
-                                 int* counters, void* stream) {
+                                 int* counters, const float2* rope_table, int lmax, int half,
+                                 float2* rope_cur, void* stream) {
   hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(64), 0, as_stream(stream), ids, B,
-                     out_tokens, out_stride, counters);
+                     out_tokens, out_stride, counters, rope_table, lmax, half, rope_cur);
   STRATA_HIP_CHECK(hipGetLastError());
   return STRATA_OK;
 }

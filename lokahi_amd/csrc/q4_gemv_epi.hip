@@ -26,6 +26,9 @@ int strata_q4_gemv_epi(strata_ctx* ctx, const void* x, int M, int K, const strat
     batch.theta = e.theta;
     STRATA_REQUIRE(e.rope_table != nullptr, "RoPE/KV epilogue needs the (cos, sin) table");
     batch.rope_table = e.rope_table;
+    STRATA_REQUIRE(e.dpos == nullptr || e.rope_cur != nullptr,
+                   "RoPE/KV epilogue with a device position needs the staged (cos, sin) row");
+    batch.rope_cur = e.rope_cur;
     batch.q_out = e.q_out;
     batch.kc = e.kc;
     batch.vc = e.vc;
@@ -41,6 +44,9 @@ int strata_q4_gemv_epi(strata_ctx* ctx, const void* x, int M, int K, const strat
       return norm ? dispatch_q4<EPI_SILU_PAIR, true, bf16_t, bf16_t>(ctx, x, M, K, batch, na, s)
                   : dispatch_q4<EPI_SILU_PAIR, false, bf16_t, bf16_t>(ctx, x, M, K, batch, na, s);
     case EPI_ROPE_KV:
+      if (e.dpos)
+        return norm ? dispatch_q4<EPI_ROPE_KV_DEV, true, bf16_t, bf16_t>(ctx, x, M, K, batch, na, s)
+                    : dispatch_q4<EPI_ROPE_KV_DEV, false, bf16_t, bf16_t>(ctx, x, M, K, batch, na, s);
       return norm ? dispatch_q4<EPI_ROPE_KV, true, bf16_t, bf16_t>(ctx, x, M, K, batch, na, s)
                   : dispatch_q4<EPI_ROPE_KV, false, bf16_t, bf16_t>(ctx, x, M, K, batch, na, s);
     default:

@@ -58,7 +58,13 @@ struct Q4Problem {
 //                   h[m, n] = bf16(h[m, n] + bf16(acc)) in place
 //                   (llama_mlx.py:647, 653); only the lane that owns row n
 //                   touches h[m, n] in the launch.
-enum { EPI_STORE = 0, EPI_SILU_PAIR = 1, EPI_ROPE_KV = 2, EPI_RESID = 3 };
+//   EPI_ROPE_KV_DEV: EPI_ROPE_KV with the position in device memory (dpos,
+//                   graph-replayed steps) and its (cos, sin) row staged in
+//                   rope_cur; a separate kernel, so the position load needs
+//                   no runtime branch.
+enum { EPI_STORE = 0, EPI_SILU_PAIR = 1, EPI_ROPE_KV = 2, EPI_RESID = 3, EPI_ROPE_KV_DEV = 4 };
+template <int EPI>
+constexpr bool kRopeEpi = EPI == EPI_ROPE_KV || EPI == EPI_ROPE_KV_DEV;
 
 // Optional RMSNorm prologue (llama_mlx.py:77-92): x is replaced by
 // bf16(w * (x * r)), r = 1/sqrt(mean(x^2) + eps) per batch row, before it is
@@ -76,6 +82,9 @@ struct Q4Batch {
   // EPI_ROPE_KV
   int head_dim, n_heads, n_kv_heads, lmax, pos0;
   const int* dpos;  // device position (graph-replayed step) or nullptr
+  // with dpos: (cos, sin) [head_dim/2] of the position *dpos, staged by the
+  // step that advanced it, so the RoPE operands need no dependent load
+  const float2* rope_cur;
   float theta;
   const float2* rope_table;  // [lmax][head_dim/2] (cos, sin) of every cache position
   uint16_t* q_out;  // [M, Hq, 1, D] bf16
@@ -185,12 +194,22 @@ __device__ __forceinline__ void xstage_load(XStage<MT, XI>& st, const uint16_t* 
                                             const uint16_t* __restrict__ norm_w = nullptr) {
 #pragma unroll
   for (int k = 0; k < XI; ++k) {
-    const int idx = min((int)(threadIdx.x + k * blockDim.x), MT * nv - 1);
+    const int raw = threadIdx.x + k * blockDim.x;
+    const int idx = min(raw, MT * nv - 1);
     const int mm = idx / nv, i = idx - mm * nv;
     const int m = min(m0 + mm, M - 1);  // rows past M are zeroed at store time
     const uint4* xr = reinterpret_cast<const uint4*>(x + (int64_t)m * K + (int64_t)i * 32);
+    // Without the RMSNorm prologue, threads without an item load nothing
+    // (their staged values are unused, see xstage_store); the prologue reads
+    // every thread's values unconditionally, which keeps its loads ahead of
+    // the weight stream, and measured faster with all threads loading.
+    if (NORM || raw < MT * nv) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) st.v[k][j] = xr[j];
+      for (int j = 0; j < 4; ++j) st.v[k][j] = xr[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) st.v[k][j] = make_uint4(0, 0, 0, 0);
+    }
     if constexpr (NORM) {
       const uint4* wr = reinterpret_cast<const uint4*>(norm_w) + i * 4;
 #pragma unroll
@@ -199,15 +218,27 @@ __device__ __forceinline__ void xstage_load(XStage<MT, XI>& st, const uint16_t* 
   }
 }
 
-template <int MT, int XI>
+// Without the RMSNorm prologue every thread stores: threads past the item
+// count write into a per-lane sink after the staged x (kXSinkBytes), so no
+// two lanes of a wave write one LDS address.  A conditional store would let
+// the compiler sink the x loads into it, behind the weight loads (which
+// return first: loads complete in order).  With the prologue the x values
+// are consumed before the store, and threads past the item count skip it.
+constexpr int kXSinkBytes = 16 + 64 * (4 * 16 + 4);  // alignment pad + per-lane sink
+template <int MT, int XI, bool NORM>
 __device__ __forceinline__ void xstage_store(const XStage<MT, XI>& st, int M, int m0, int nv,
                                              uint4* smem) {
   uint4* xq = smem;
   float* xs = reinterpret_cast<float*>(smem + MT * 4 * nv);
+  uint4* sink_q = smem + MT * 4 * nv + (MT * nv + 3) / 4;  // first 16-byte slot after xs
+  float* sink_s = reinterpret_cast<float*>(sink_q + 4 * 64);
+  const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int k = 0; k < XI; ++k) {
-    const int idx = threadIdx.x + k * blockDim.x;
-    if (idx >= MT * nv) break;
+    const int raw = threadIdx.x + k * blockDim.x;
+    const bool item = raw < MT * nv;
+    if (NORM && !item) break;
+    const int idx = min(raw, MT * nv - 1);
     const int mm = idx / nv, i = idx - mm * nv;
     const bool live = m0 + mm < M;
     float sum = 0.f;
@@ -219,13 +250,13 @@ __device__ __forceinline__ void xstage_store(const XStage<MT, XI>& st, int M, in
       pr.y = (v.x >> 16) | (v.z & 0xffff0000u);
       pr.z = (v.y & 0xffffu) | (v.w << 16);
       pr.w = (v.y >> 16) | (v.w & 0xffff0000u);
-      xq[(mm * 4 + j) * nv + i] = pr;
+      *(item ? &xq[(mm * 4 + j) * nv + i] : &sink_q[j * 64 + lane]) = pr;
       const uint32_t u[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         sum += __uint_as_float(u[c] << 16) + __uint_as_float(u[c] & 0xffff0000u);
     }
-    xs[mm * nv + i] = sum;
+    *(item ? &xs[mm * nv + i] : &sink_s[lane]) = sum;
   }
 }
 
@@ -321,7 +352,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(kFiveWa
 void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
                                                           Q4Batch batch, NormArgs na) {
   static_assert(!NORM || XI > 0, "the RMSNorm prologue needs split bf16 staging");
-  static_assert((EPI != EPI_SILU_PAIR && EPI != EPI_ROPE_KV) || R == 2,
+  static_assert((EPI != EPI_SILU_PAIR && !kRopeEpi<EPI>) || R == 2,
                 "pair epilogues need two rows per wave");
   extern __shared__ uint4 smem[];
   const int nv = K >> 5;  // uint4 (32 codes) per weight row
@@ -341,8 +372,24 @@ void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
   // Epilogue operands are fetched with the block's weights, not at the tail:
   // the RoPE position and (cos, sin) of the block's pair, and the residual
   // values h[m, n] the RESID epilogue adds to.
+  // EPI_ROPE_KV_DEV (graph-replayed step): the (cos, sin) pair comes from
+  // the staged row rope_cur, and the position, needed only for the KV-append
+  // address, is read after the weight loads are issued (load_rope_pos).  It
+  // is a vector load from the global address space (a zero offset held in a
+  // VGPR keeps it off the scalar path): a generic or scalar load counts on the
+  // LDS wait counter too, so every wave would stall on it before issuing its
+  // x and weight loads or in the RMSNorm prologue's LDS waits.
+  // EPI_ROPE_KV: the position is the argument pos0.
   int rope_pos = 0;
-  if constexpr (EPI == EPI_ROPE_KV) rope_pos = batch.dpos ? *batch.dpos : batch.pos0;
+  if constexpr (EPI == EPI_ROPE_KV) rope_pos = batch.pos0;
+  auto load_rope_pos = [&]() {
+    if constexpr (EPI == EPI_ROPE_KV_DEV) {
+      using gint = const __attribute__((address_space(1))) int;
+      int zero;
+      asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+      rope_pos = ((gint*)batch.dpos)[zero];
+    }
+  };
   float2 cs_pre = make_float2(0.f, 0.f);
   uint16_t h_pre[R][MT];
   auto setup = [&](int b) {
@@ -359,7 +406,7 @@ void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
       for (int t = 1; t < kMaxProblems; ++t)
         if (t < batch.count && row >= batch.p[t].row0) pi = t;
       n = valid[r] ? row - batch.p[pi].row0 : 0;
-      if constexpr (EPI == EPI_ROPE_KV) {  // (h, 2p + w) -> h*D + p + w*D/2
+      if constexpr (kRopeEpi<EPI>) {  // (h, 2p + w) -> h*D + p + w*D/2
         const int D = batch.head_dim, j = n % D;
         n = n - j + (j >> 1) + (j & 1) * (D >> 1);
       }
@@ -378,12 +425,14 @@ void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
     }
   }
   };
-  // The (cos, sin) load depends on the position load: issue it after the
-  // block's weight loads so they do not queue behind it.
+  // Issued after the block's weight loads, so they do not queue behind it.
   auto prefetch_rope = [&]() {
-    if constexpr (EPI == EPI_ROPE_KV) {
-      const int D = batch.head_dim, i = nloc[0] % D;  // pair (i, i + D/2), i < D/2
-      cs_pre = batch.rope_table[(int64_t)rope_pos * (D >> 1) + min(i, (D >> 1) - 1)];
+    if constexpr (kRopeEpi<EPI>) {
+      const int D = batch.head_dim, i = min(nloc[0] % D, (D >> 1) - 1);  // pair (i, i + D/2)
+      if constexpr (EPI == EPI_ROPE_KV_DEV)
+        cs_pre = batch.rope_cur[i];
+      else
+        cs_pre = batch.rope_table[(int64_t)rope_pos * (D >> 1) + i];
     }
   };
   setup(blk);
@@ -480,13 +529,15 @@ void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
     xstage_load<MT, XI, NORM>(st, reinterpret_cast<const uint16_t*>(x), M, K, m0, nv, na.w);
     issue(0);
     prefetch_rope();
+    load_rope_pos();
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (NORM) xstage_norm<NW, MT, XI>(st, M, K, m0, nv, na);
-    xstage_store<MT, XI>(st, M, m0, nv, smem);
+    xstage_store<MT, XI, NORM>(st, M, m0, nv, smem);
   } else {
     stage_x<XT, MT>(x, M, K, m0, smem, nv);
     issue(0);
     prefetch_rope();
+    load_rope_pos();
   }
   __syncthreads();
   // Persistent over row blocks (grid-stride): x is staged once per
@@ -522,7 +573,7 @@ void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int mm = 0; mm < MT; ++mm) acc[r][mm] = wave_sum(acc[r][mm]);
-  if constexpr (EPI == EPI_SILU_PAIR || EPI == EPI_ROPE_KV) {
+  if constexpr (EPI == EPI_SILU_PAIR || kRopeEpi<EPI>) {
     {
 #pragma unroll
       for (int mm = 0; mm < MT; ++mm) {
@@ -739,7 +790,7 @@ bool launch_q4_u(const GemvShape& g, const void* x, int M, int K, const Q4Batch&
                  const NormArgs& na, size_t lds, hipStream_t s) {
   // Kernels with the RMSNorm prologue or a pair epilogue run at the hidden
   // width only (K <= 8192, U <= 4); fp32 activations use U = 4.
-  constexpr bool kSmall = NORM || EPI == EPI_SILU_PAIR || EPI == EPI_ROPE_KV;
+  constexpr bool kSmall = NORM || EPI == EPI_SILU_PAIR || kRopeEpi<EPI>;
   constexpr bool kF32 = sizeof(XT) == 4;
   if (g.u == 2 && !kF32) {
     launch_q4_k<NW, R, 2, MT, EPI, NORM, XT, YT>(x, M, K, batch, na, lds, s);
@@ -767,13 +818,13 @@ bool launch_q4_u(const GemvShape& g, const void* x, int M, int K, const Q4Batch&
 template <int EPI, bool NORM, typename XT, typename YT>
 int dispatch_q4(strata_ctx* ctx, const void* x, int M, int K, const Q4Batch& batch,
                 const NormArgs& na, hipStream_t stream) {
-  constexpr bool kPair = EPI == EPI_SILU_PAIR || EPI == EPI_ROPE_KV;
+  constexpr bool kPair = EPI == EPI_SILU_PAIR || kRopeEpi<EPI>;
   g_num_cus = ctx->num_cus;
   const int nv = K / 32;
   GemvShape g = pick_shape(nv, batch.total_rows, M);
   const size_t per_row = (size_t)nv * ((sizeof(XT) == 2 ? 64 : 128) + 4);
-  while (g.mt > 1 && g.mt * per_row > (size_t)ctx->max_lds_per_block) g.mt /= 2;
-  const size_t lds = g.mt * per_row;
+  while (g.mt > 1 && g.mt * per_row + kXSinkBytes > (size_t)ctx->max_lds_per_block) g.mt /= 2;
+  const size_t lds = g.mt * per_row + kXSinkBytes;
   STRATA_REQUIRE((int64_t)lds <= ctx->max_lds_per_block,
                  "q4 GEMV: K=%d needs %zu B of LDS, device allows %d", K, lds,
                  ctx->max_lds_per_block);

@@ -25,6 +25,7 @@ struct GemvEpilogue {
   const uint16_t* norm_w;
   float eps;
   const float2* rope_table;  // (cos, sin) table [lmax][head_dim/2], required by mode 2
+  const float2* rope_cur;    // with dpos: (cos, sin) [head_dim/2] of position *dpos
 };
 int strata_q4_gemv_epi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
                        int count, const GemvEpilogue& e, void* stream);
@@ -75,8 +76,11 @@ int strata_quantize_launch(const void* src, int dtype, int64_t N, int64_t K, int
 // (cos, sin) of RoPE for positions 0..lmax-1 and pairs 0..D/2-1, evaluated
 // exactly as the in-kernel RoPE evaluates them (bit-identical).
 int strata_rope_table_launch(float2* table, int lmax, int D, float theta, void* stream);
+// Records the step's tokens, advances {step, position, key count} and, when
+// rope_cur is given, stages rope_table's row of the new position into it.
 int strata_decode_advance_launch(const int32_t* ids, int B, int32_t* out_tokens, int out_stride,
-                                 int* counters, void* stream);
+                                 int* counters, const float2* rope_table, int lmax, int half,
+                                 float2* rope_cur, void* stream);
 
 struct strata_kv {
   strata_ctx* ctx;
