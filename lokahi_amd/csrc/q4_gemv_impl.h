@@ -721,7 +721,8 @@ struct GemvShape {
 GemvShape pick_shape(int nv, int rows, int M) {
   // Measured on MI355X (graph-replayed launches, weights cycled past the
   // 256 MB last-level cache): K=4096 rows prefer 4 waves x 2 rows with U=2,
-  // small launches 8 waves x 1 row; batch-1 K=14336 prefers 8 waves x 1 row
+  // small launches (< 8192 rows) 4 waves x 1 row (q/k/v 6.5 -> 5.8 us against
+  // 8 waves x 1 row); batch-1 K=14336 prefers 8 waves x 1 row
   // with U=4 over two K chunks, one row block per workgroup (9.9 us against
   // 10.7 us for 4 waves with U=7 in one chunk).
   GemvShape g;
@@ -732,7 +733,7 @@ GemvShape pick_shape(int nv, int rows, int M) {
     g.r = 2;
     g.nw = 4;
   } else if (g.u == 2) {
-    g.nw = rows < 8192 ? 8 : 4;
+    g.nw = 4;
     g.r = rows < 8192 ? 1 : 2;
   } else {
     g.nw = 8;
