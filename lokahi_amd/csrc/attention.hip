@@ -165,10 +165,23 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   }
   const int t1 = min(kend, t0 + chunk);
 
-  float qv[G][EPL];
+  // bf16 q and K: q stays packed and q.k runs on v_dot2_f32_bf16 over the
+  // raw K words (no K conversion, half the q registers); otherwise fp32 FMAs.
+  constexpr bool kDot2 = sizeof(TQ) == 2 && sizeof(TK) == 2;
+  float qv[G][kDot2 ? 1 : EPL];
+  uint32_t qw[G][kDot2 ? EPL / 2 : 1];
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-    load_elems<TQ, EPL>(q + ((int64_t)b * Hq + hq0 + g) * D + e0, qv[g]);
+  for (int g = 0; g < G; ++g) {
+    const TQ* qp = q + ((int64_t)b * Hq + hq0 + g) * D + e0;
+    if constexpr (kDot2) {
+      Raw<TQ, EPL> r;
+      r.load(qp);
+#pragma unroll
+      for (int w = 0; w < EPL / 2; ++w) qw[g][w] = r.u[w];
+    } else {
+      load_elems<TQ, EPL>(qp, qv[g]);
+    }
+  }
 
   float m[G], s[G], o[G][EPL];
 #pragma unroll
@@ -181,10 +194,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 
   const float sl2 = scale * kLog2e;
   auto consume = [&](const RK* kr, const RV* vr, int base) {
-    float kx[J][EPL], vx[J][EPL];
+    float kx[J][kDot2 ? 1 : EPL], vx[J][EPL];
 #pragma unroll
     for (int jj = 0; jj < J; ++jj) {
-      kr[jj].to_float(kx[jj]);
+      if constexpr (!kDot2) kr[jj].to_float(kx[jj]);
       vr[jj].to_float(vx[jj]);
       // Keys past the count were fetched speculatively (any bits, NaN
       // included): their weight is 0, and 0 * NaN must not reach o.
@@ -200,8 +213,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
       for (int jj = 0; jj < J; ++jj) {
         float d = 0.f;
+        if constexpr (kDot2) {
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) d = fmaf(qv[g][e], kx[jj][e], d);
+          for (int w = 0; w < EPL / 2; ++w)
+            d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kr[jj].u[w]),
+                                                __builtin_bit_cast(bf16x2_t, qw[g][w]), d, false);
+        } else {
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) d = fmaf(qv[g][e], kx[jj][e], d);
+        }
         d = group_sum<LPK>(d);
         sc[jj] = (base + jj * 4 * KPW + sub < t1) ? d * sl2 : -INFINITY;  // log2 domain
         mb = fmaxf(mb, sc[jj]);
