@@ -593,6 +593,12 @@ void attn_prefill_mfma(
       }
     }
   };
+  // Element offset of 4-key column block c4 of row d in the transposed V
+  // tile.  The block index is XORed with (d >> 5) & 3: the staging stores of
+  // 32 lanes (head-dim blocks 0..31, rows 4 apart) otherwise meet every 8
+  // lanes on the same banks; a 16-row read group never crosses 32 rows, so
+  // the MFMA operand reads keep their pattern.
+  auto vt_at = [&](int d, int c4) { return d * (KT + VPAD) + 4 * (c4 ^ ((d >> 5) & 3)); };
   // ---- stage K (row-major, padded) and V (bf16: transposed) tiles
   auto stage = [&](int buf) {
 #pragma unroll
@@ -619,7 +625,7 @@ void attn_prefill_mfma(
             make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, hi), __builtin_amdgcn_perm(r[3].y, r[2].y, hi))};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          *reinterpret_cast<uint2*>(&vt[(4 * dg + j) * (KT + VPAD) + 4 * kg]) = o[j];
+          *reinterpret_cast<uint2*>(&vt[vt_at(4 * dg + j, kg)]) = o[j];
       }
     }
   };
@@ -748,9 +754,9 @@ void attn_prefill_mfma(
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const uint16_t* vr = vt + (dt * 16 + col) * (KT + VPAD);
-          const uint2 lo = *reinterpret_cast<const uint2*>(vr + 32 * c2 + 4 * grp);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 32 * c2 + 16 + 4 * grp);
+          const int d = dt * 16 + col;
+          const uint2 lo = *reinterpret_cast<const uint2*>(vt + vt_at(d, 8 * c2 + grp));
+          const uint2 hi = *reinterpret_cast<const uint2*>(vt + vt_at(d, 8 * c2 + 4 + grp));
           const bf16x8_t a = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
