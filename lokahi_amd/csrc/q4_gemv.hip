@@ -30,19 +30,26 @@ int strata_bf16_gemv(strata_ctx* ctx, const void* x, int M, int K, const uint16_
   hipStream_t s = as_stream(stream);
   const uint16_t* xx = reinterpret_cast<const uint16_t*>(x);
   const uint4* ww = reinterpret_cast<const uint4*>(w);
-#define STRATA_BF16_LAUNCH(MTV)                                                                 \
-  if (MT == MTV) {                                                                              \
-    if (y_dtype == STRATA_F32)                                                                  \
-      hipLaunchKernelGGL((bf16_gemv_kernel<NW, R, U, MTV, float>), grid, dim3(NW * 64), lds, s, \
-                         xx, M, K, ww, N, reinterpret_cast<float*>(y));                         \
-    else                                                                                        \
-      hipLaunchKernelGGL((bf16_gemv_kernel<NW, R, U, MTV, bf16_t>), grid, dim3(NW * 64), lds,   \
-                         s, xx, M, K, ww, N, reinterpret_cast<bf16_t*>(y));                     \
+  // x ahead of the weights when each batch row is one uint4 per thread
+  // (K = 4096: the lm_head of the Llama-3-8B shape)
+  const int xi = K / 8 == NW * 64 ? MT : 0;
+#define STRATA_BF16_LAUNCH(MTV, XIV)                                                           \
+  if (MT == MTV && xi == XIV) {                                                                \
+    if (y_dtype == STRATA_F32)                                                                 \
+      hipLaunchKernelGGL((bf16_gemv_kernel<NW, R, U, MTV, float, XIV>), grid, dim3(NW * 64),   \
+                         lds, s, xx, M, K, ww, N, reinterpret_cast<float*>(y));                \
+    else                                                                                       \
+      hipLaunchKernelGGL((bf16_gemv_kernel<NW, R, U, MTV, bf16_t, XIV>), grid, dim3(NW * 64),  \
+                         lds, s, xx, M, K, ww, N, reinterpret_cast<bf16_t*>(y));               \
+    STRATA_HIP_CHECK(hipGetLastError());                                                       \
+    return STRATA_OK;                                                                          \
   }
-  STRATA_BF16_LAUNCH(1)
-  STRATA_BF16_LAUNCH(2)
-  STRATA_BF16_LAUNCH(4)
+  STRATA_BF16_LAUNCH(1, 1)
+  STRATA_BF16_LAUNCH(1, 0)
+  STRATA_BF16_LAUNCH(2, 2)
+  STRATA_BF16_LAUNCH(2, 0)
+  STRATA_BF16_LAUNCH(4, 4)
+  STRATA_BF16_LAUNCH(4, 0)
 #undef STRATA_BF16_LAUNCH
-  STRATA_HIP_CHECK(hipGetLastError());
-  return STRATA_OK;
+  return strata_set_error(STRATA_EINVAL, "bf16 GEMV: no kernel for batch tile %d", MT);
 }

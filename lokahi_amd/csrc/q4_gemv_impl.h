@@ -638,8 +638,11 @@ void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
 }
 
 // Dense bf16-weight GEMV (lm_head): y[m,n] = sum_k x[m,k] * W[n,k]; same
-// load-first structure, one uint4 = 8 weights per lane per step.
-template <int NW, int R, int U, int MT, typename YT>
+// load-first structure, one uint4 = 8 weights per lane per step.  XI > 0:
+// the MT*K/8 x items are exactly XI per thread and are loaded before the
+// weight stream (loads return in order: x staged after the weights would
+// wait for all of them); XI = 0 stages x after the first weight loads.
+template <int NW, int R, int U, int MT, typename YT, int XI = 0>
 __global__ __launch_bounds__(NW * 64) void bf16_gemv_kernel(const uint16_t* __restrict__ x, int M,
                                                             int K, const uint4* __restrict__ w,
                                                             int N, YT* __restrict__ y) {
@@ -654,6 +657,17 @@ __global__ __launch_bounds__(NW * 64) void bf16_gemv_kernel(const uint16_t* __re
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int mm = 0; mm < MT; ++mm) acc[r][mm] = 0.f;
+  uint4 xr[XI > 0 ? XI : 1];
+  if constexpr (XI > 0) {
+#pragma unroll
+    for (int k = 0; k < XI; ++k) {
+      const int idx = threadIdx.x + k * NW * 64;
+      const int mm = idx / nv, i = idx - mm * nv;
+      const int m = min(m0 + mm, M - 1);  // rows past M are zeroed at store time
+      xr[k] = reinterpret_cast<const uint4*>(x + (int64_t)m * K)[i];
+      if (m0 + mm >= M) xr[k] = make_uint4(0, 0, 0, 0);
+    }
+  }
   for (int c0 = 0; c0 < nv; c0 += 64 * U) {
     uint4 wv[R][U];
 #pragma unroll
@@ -668,11 +682,16 @@ __global__ __launch_bounds__(NW * 64) void bf16_gemv_kernel(const uint16_t* __re
       }
     }
     if (c0 == 0) {
-      for (int idx = threadIdx.x; idx < MT * nv; idx += blockDim.x) {
-        const int mm = idx / nv, i = idx - mm * nv;
-        const int m = m0 + mm;
-        smem[idx] = (m < M) ? reinterpret_cast<const uint4*>(x + (int64_t)m * K)[i]
-                            : make_uint4(0, 0, 0, 0);
+      if constexpr (XI > 0) {
+#pragma unroll
+        for (int k = 0; k < XI; ++k) smem[threadIdx.x + k * NW * 64] = xr[k];
+      } else {
+        for (int idx = threadIdx.x; idx < MT * nv; idx += blockDim.x) {
+          const int mm = idx / nv, i = idx - mm * nv;
+          const int m = m0 + mm;
+          smem[idx] = (m < M) ? reinterpret_cast<const uint4*>(x + (int64_t)m * K)[i]
+                              : make_uint4(0, 0, 0, 0);
+        }
       }
       __syncthreads();
     }
