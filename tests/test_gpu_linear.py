@@ -136,7 +136,10 @@ def test_linear_rejects_bad_parameters(dev):
 def test_bf16_dense_linear(dev):
     from lokahi_amd import ops
     rng = np.random.default_rng(12)
-    for M, N, K in [(1, 1000, 512), (3, 333, 256)]:
+    # K = 4096 takes the x-ahead-of-weights kernels (batch tiles 1, 2, 4;
+    # M = 5 leaves three zeroed rows in its second tile)
+    for M, N, K in [(1, 1000, 512), (3, 333, 256), (1, 777, 4096), (2, 500, 4096),
+                    (4, 300, 4096), (5, 130, 4096)]:
         W = f32_to_bf16_bits(rng.normal(0, 0.02, (N, K)).astype(np.float32))
         x = f32_to_bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
         y = to_np_f32(ops.linear(to_dev(x, dev), to_dev(W, dev), None, None, out_dtype=torch.float32))
