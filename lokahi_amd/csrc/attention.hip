@@ -860,12 +860,13 @@ __global__ __launch_bounds__(64) void attn_generic(
 
 // Key-axis split of the decode kernel for `Lcap` keys: enough workgroups to
 // cover the GPU about 4x, at least 64 keys (one 4-wave sweep) per split
-// below 2048 keys and 128 from there on, at most kMaxDecodeSplits splits.
-// At batch 1 the kernel is bound by each wave's dependent VALU chain, so
-// short splits (more waves) win up to ~1k keys; from 2k keys two sweeps per
-// split halve the merge's work and measured 0.6-0.8 us faster
-// (STRATA_ATTN_MIN_CHUNK overrides the minimum).
-constexpr int kLongSplitKeys = 2048;
+// below 3072 keys and 128 from there on, at most kMaxDecodeSplits splits.
+// At batch 1 the kernel is bound by each wave's dependent chain, so short
+// splits (more waves) win up to ~2.3k keys (2k: 7.6 us against 8.2 us); from
+// 4k keys two sweeps per split halve the merge's work (4k: 10.1 us against
+// 11.4 us; 8k: 15.5 us against 17.4 us) (STRATA_ATTN_MIN_CHUNK overrides the
+// minimum).
+constexpr int kLongSplitKeys = 3072;
 void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
   int min_chunk = Lcap >= kLongSplitKeys ? 128 : 64;
   if (const char* e = getenv("STRATA_ATTN_MIN_CHUNK")) min_chunk = std::max(64, atoi(e));
@@ -905,12 +906,13 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
     }
   }
   // Query heads per workgroup: the whole group reads K/V once; while the grid
-  // has fewer workgroups than CUs (short contexts) the group is halved, so
-  // each wave's chain is shorter (measured at 64-1024 keys: 1-1.6 us faster;
-  // at 2k+ keys the full group is as fast or faster).
+  // has fewer than two workgroups per CU the group is halved, so each wave's
+  // chain is shorter (batch 1: 1k keys 1 head, 2k-4k keys 2 heads per
+  // workgroup: 2k 8.6 -> 7.6 us, 4k 10.7 -> 10.1 us; 8k+ and batch 16 keep
+  // the full group, which reads K/V once).
   // STRATA_ATTN_HEADS_PER_WG picks a divisor of the group instead.
   int HG = G;
-  while (HG % 2 == 0 && (int64_t)nsplit * B * Hkv * (G / HG) < ctx->num_cus) HG /= 2;
+  while (HG % 2 == 0 && (int64_t)nsplit * B * Hkv * (G / HG) < 2 * ctx->num_cus) HG /= 2;
   if (const char* e = getenv("STRATA_ATTN_HEADS_PER_WG")) {
     const int h = atoi(e);
     if (h > 0 && G % h == 0 && (h == 1 || h == 2 || h == 3 || h == 4 || h == 6 || h == 8)) HG = h;
