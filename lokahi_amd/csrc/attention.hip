@@ -867,15 +867,21 @@ __global__ __launch_bounds__(64) void attn_generic(
 // 11.4 us; 8k: 15.5 us against 17.4 us) (STRATA_ATTN_MIN_CHUNK overrides the
 // minimum).
 constexpr int kLongSplitKeys = 3072;
+constexpr int kLongContextKeys = 12288;
 void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
   int min_chunk = Lcap >= kLongSplitKeys ? 128 : 64;
   if (const char* e = getenv("STRATA_ATTN_MIN_CHUNK")) min_chunk = std::max(64, atoi(e));
   // Batched heads (B*Hkv >= 64, e.g. 16 x 8): short contexts prefer longer
   // splits (1k keys: 21.6 us at 2 per CU against 24.0 at 4), very long ones
-  // more of them (32k keys: 371 us at 6 against 378 at 4).  The count stays
-  // non-decreasing in Lcap, which the partials sizing relies on.
+  // more of them (32k keys: 371 us at 6 against 378 at 4).  Few heads (batch
+  // 1): from 12k keys longer splits (16k: 21.3 us at 2 per CU against 24.3;
+  // 32k: 30.0 against 34.4).  strata_attn_decode_splits takes the maximum
+  // over these regimes' boundaries for the partials sizing.
   int per_cu = 4;
-  if (B * Hkv >= 64) per_cu = Lcap <= 2048 ? 2 : (Lcap >= 16384 ? 6 : 4);
+  if (B * Hkv >= 64)
+    per_cu = Lcap <= 2048 ? 2 : (Lcap >= 16384 ? 6 : 4);
+  else if (Lcap >= kLongContextKeys)
+    per_cu = 2;
   if (const char* e = getenv("STRATA_ATTN_SPLITS_PER_CU")) per_cu = std::max(1, atoi(e));
   int want = (num_cus * per_cu + B * Hkv - 1) / (B * Hkv);
   if (want > kMaxDecodeSplits) want = kMaxDecodeSplits;
@@ -994,12 +1000,16 @@ int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v,
 int strata_attn_decode_splits(strata_ctx* ctx, int B, int Hkv, int Lcap) {
   int nsplit, chunk;
   decode_split_geometry(ctx->num_cus, B, Hkv, Lcap, &nsplit, &chunk);
-  // The split count grows with the capacity within each minimum-chunk regime;
-  // the largest capacity below the switch may need more splits than Lcap.
-  if (Lcap >= kLongSplitKeys) {
-    int n2;
-    decode_split_geometry(ctx->num_cus, B, Hkv, kLongSplitKeys - 1, &n2, &chunk);
-    nsplit = std::max(nsplit, n2);
+  // The split count grows with the capacity within each regime of the
+  // geometry (minimum chunk, splits per CU); the last capacity before a
+  // regime boundary may need more splits than Lcap.
+  const int bounds[] = {2048, kLongSplitKeys - 1, kLongContextKeys - 1, 16383};
+  for (int bnd : bounds) {
+    if (Lcap > bnd) {
+      int n2;
+      decode_split_geometry(ctx->num_cus, B, Hkv, bnd, &n2, &chunk);
+      nsplit = std::max(nsplit, n2);
+    }
   }
   return nsplit;
 }
