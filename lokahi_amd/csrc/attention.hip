@@ -867,15 +867,16 @@ __global__ __launch_bounds__(64) void attn_generic(
 // 11.4 us; 8k: 15.5 us against 17.4 us) (STRATA_ATTN_MIN_CHUNK overrides the
 // minimum).
 constexpr int kLongSplitKeys = 3072;
-constexpr int kLongContextKeys = 12288;
+constexpr int kLongContextKeys = 6144;
 void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
   int min_chunk = Lcap >= kLongSplitKeys ? 128 : 64;
   if (const char* e = getenv("STRATA_ATTN_MIN_CHUNK")) min_chunk = std::max(64, atoi(e));
   // Batched heads (B*Hkv >= 64, e.g. 16 x 8): short contexts prefer longer
   // splits (1k keys: 21.6 us at 2 per CU against 24.0 at 4), very long ones
   // more of them (32k keys: 371 us at 6 against 378 at 4).  Few heads (batch
-  // 1): from 12k keys longer splits (16k: 21.3 us at 2 per CU against 24.3;
-  // 32k: 30.0 against 34.4).  strata_attn_decode_splits takes the maximum
+  // 1): from 6k keys longer splits (8k: 13.9 us at 2 per CU against 16.0;
+  // 16k: 21.3 against 24.3; 32k: 30.0 against 34.4; below 8k the 128-key
+  // minimum already bounds the count).  strata_attn_decode_splits takes the maximum
   // over these regimes' boundaries for the partials sizing.
   int per_cu = 4;
   if (B * Hkv >= 64)
