@@ -143,3 +143,22 @@ def test_engine_ignores_unwritten_cache_slots(dev):
     got = eng.generate(torch.from_numpy(prompt), 10).cpu().numpy()
     exp = oll.greedy_generate(ref, prompt, max_new_tokens=10, cache=OracleKVCache(2))
     assert np.array_equal(got, exp), f"\n{got[:, 61:]}\n{exp[:, 61:]}"
+
+
+LONG8 = oll.Config(vocab_size=256, hidden_size=512, intermediate_size=512, num_hidden_layers=1,
+                   num_attention_heads=8, num_key_value_heads=8, rms_norm_eps=1e-5,
+                   rope_theta=500000.0)
+
+
+def test_engine_long_context_across_split_regimes(dev):
+    """8 KV heads at batch 1, decoding from 5800 to 6200 keys: the step graphs
+    of the 5888, 6144 and 6400-key buckets use different split-K geometries
+    (4 workgroups per CU below 6144 keys, 2 from there), all served by the
+    decoder's one partials buffer.  The graph-replayed steps (device-held
+    position) must give the host-launched steps' tokens exactly."""
+    model, _ = _pair(LONG8, seed=47, std=0.05)
+    prompt = torch.from_numpy(np.random.default_rng(47).integers(0, LONG8.vocab_size, (1, 5800)))
+    a = model.generate(prompt, max_new_tokens=400, use_graph=True).cpu()
+    b = model.generate(prompt, max_new_tokens=400, use_graph=False).cpu()
+    assert a.shape == (1, 6200)
+    assert torch.equal(a, b)
