@@ -653,6 +653,9 @@ void attn_prefill_mfma(
       live[qb] = kb0 < need;
     }
 
+    // MFMA sections run at raised wave priority, so the other wave of the
+    // SIMD fills the matrix core's gaps with its softmax.
+    if constexpr (kBF16) __builtin_amdgcn_s_setprio(1);
     // ---- S^T tiles: st[qb][j][i] = score(query row of block qb, key kb0 + 16j + 4*grp + i)
     f32x4_t st[QB][4];
 #pragma unroll
@@ -678,6 +681,7 @@ void attn_prefill_mfma(
       }
     }
 
+    if constexpr (kBF16) __builtin_amdgcn_s_setprio(0);
     // ---- online softmax (log2 domain), all state for this lane's query rows.
     // Raw scores are kept; the scale goes into the exponent's FMA
     // (sl2 > 0, so max(s * sl2) = sl2 * max(s)).  Tiles every row of the
@@ -737,6 +741,7 @@ void attn_prefill_mfma(
       }
     }
 
+    if constexpr (kBF16) __builtin_amdgcn_s_setprio(1);
     // ---- O^T += V^T P^T
     if constexpr (kBF16) {
       const uint16_t* vt = reinterpret_cast<const uint16_t*>(vs);
@@ -778,6 +783,7 @@ void attn_prefill_mfma(
           }
         }
     }
+    if constexpr (kBF16) __builtin_amdgcn_s_setprio(0);
     if constexpr (NBUF == 2) {
       if (more) stage(cur ^ 1);  // the other buffer: last read before the previous barrier
       __syncthreads();
