@@ -546,7 +546,9 @@ void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
   for (;;) {
   compute(0);
   for (int c0 = 64 * U; c0 < nv; c0 += 64 * U) {
+    __builtin_amdgcn_s_setprio(1);
     issue(c0);
+    __builtin_amdgcn_s_setprio(0);
     compute(c0);
   }
   int e_pid[R], e_nloc[R];
@@ -564,9 +566,12 @@ void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
   const int next = blk + gridDim.x;
   const bool more = next < nblk;
   if (more) {
+    // the next block's loads go out ahead of other waves' math on the SIMD
+    __builtin_amdgcn_s_setprio(1);
     setup(next);
     issue(0);
     prefetch_rope();
+    __builtin_amdgcn_s_setprio(0);
   }
 
 #pragma unroll
