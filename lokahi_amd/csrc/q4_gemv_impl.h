@@ -531,8 +531,13 @@ void q4_gemv_kernel(const XT* __restrict__ x, int M, int K,
     prefetch_rope();
     load_rope_pos();
     __builtin_amdgcn_sched_barrier(0);
+    // x staging (and the RMSNorm) at raised wave priority: it gates every
+    // wave's first compute, while the weights are still in flight
+    // (GEMV set 30.7 -> 29.5 us, decode -2%)
+    __builtin_amdgcn_s_setprio(1);
     if constexpr (NORM) xstage_norm<NW, MT, XI>(st, M, K, m0, nv, na);
     xstage_store<MT, XI, NORM>(st, M, m0, nv, smem);
+    __builtin_amdgcn_s_setprio(0);
   } else {
     stage_x<XT, MT>(x, M, K, m0, smem, nv);
     issue(0);
