@@ -785,8 +785,8 @@ int g_num_cus = 256;
 int grid_cap(int nw, int u, bool norm, bool five_waves) {
   int per_cu = u >= 7 ? 3 : (nw >= 8 ? 6 : (five_waves ? 5 : 4));
   if (const char* e = getenv("STRATA_GEMV_WGS_PER_CU")) per_cu = atoi(e);
-  if (norm) {  // each workgroup normalizes x itself: 4 per CU measured best
-    per_cu = 4;
+  if (norm) {  // each workgroup normalizes x itself: 5 per CU measured best
+    per_cu = 5;  // (with the prologue at raised wave priority; 4 before it)
     if (const char* e = getenv("STRATA_GEMV_NORM_WGS_PER_CU")) per_cu = atoi(e);
   }
   return std::max(1, per_cu) * g_num_cus;
