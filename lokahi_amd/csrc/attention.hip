@@ -872,8 +872,10 @@ __global__ __launch_bounds__(64) void attn_generic(
 // 4k keys two sweeps per split halve the merge's work (4k: 10.1 us against
 // 11.4 us; 8k: 15.5 us against 17.4 us) (STRATA_ATTN_MIN_CHUNK overrides the
 // minimum).
-constexpr int kLongSplitKeys = 3072;
-constexpr int kLongContextKeys = 6144;
+constexpr int kLongSplitKeys = 3072;    // 128-key minimum split from here
+constexpr int kLongContextKeys = 6144;  // few heads: 2 splits per CU from here
+constexpr int kBatchedShortKeys = 2048; // batched heads: 2 per CU up to here
+constexpr int kBatchedLongKeys = 16384; // batched heads: 6 per CU from here
 void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
   int min_chunk = Lcap >= kLongSplitKeys ? 128 : 64;
   if (const char* e = getenv("STRATA_ATTN_MIN_CHUNK")) min_chunk = std::max(64, atoi(e));
@@ -886,7 +888,7 @@ void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_ou
   // over these regimes' boundaries for the partials sizing.
   int per_cu = 4;
   if (B * Hkv >= 64)
-    per_cu = Lcap <= 2048 ? 2 : (Lcap >= 16384 ? 6 : 4);
+    per_cu = Lcap <= kBatchedShortKeys ? 2 : (Lcap >= kBatchedLongKeys ? 6 : 4);
   else if (Lcap >= kLongContextKeys)
     per_cu = 2;
   if (const char* e = getenv("STRATA_ATTN_SPLITS_PER_CU")) per_cu = std::max(1, atoi(e));
@@ -1010,7 +1012,8 @@ int strata_attn_decode_splits(strata_ctx* ctx, int B, int Hkv, int Lcap) {
   // The split count grows with the capacity within each regime of the
   // geometry (minimum chunk, splits per CU); the last capacity before a
   // regime boundary may need more splits than Lcap.
-  const int bounds[] = {2048, kLongSplitKeys - 1, kLongContextKeys - 1, 16383};
+  const int bounds[] = {kBatchedShortKeys, kLongSplitKeys - 1, kLongContextKeys - 1,
+                        kBatchedLongKeys - 1};
   for (int bnd : bounds) {
     if (Lcap > bnd) {
       int n2;
