@@ -239,27 +239,33 @@ def prefill_8b():
                           "frac_mfma_bf16": round(aflops / aus / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}}
 
 
-def run_decode(cfg, prompt_len, new_tokens, seed, batch=1):
+def run_decode(cfg, prompt_len, new_tokens, seed, batch=1, warm_tokens=None):
     """Prefill `prompt_len` uniform-random ids per row, then time `new_tokens`
-    greedy tokens per row on the native engine (warm pass first, so the step
-    graphs exist)."""
+    greedy decode steps per row on the native engine.
+
+    An untimed pass first runs the same prefill and `warm_tokens` decode steps
+    (default: `new_tokens`); it also captures the step graph of each 256-key
+    bucket it reaches.  A bucket the timed pass reaches first is captured
+    inside the timed region.  Each decode step is one forward of one token
+    per row (the first from the prefill's last prompt token)."""
     import torch
     from lokahi_amd.llama import DecoderEngine, HipLlamaForCausalLM, random_weights
+    warm_tokens = new_tokens if warm_tokens is None else warm_tokens
     weights = random_weights(cfg, seed=seed)
     model = HipLlamaForCausalLM(cfg, weights)
-    cache = model.new_cache(batch, prompt_len + new_tokens + 8)
+    cache = model.new_cache(batch, prompt_len + max(new_tokens, warm_tokens) + 8)
     engine = DecoderEngine(model, cache, max_batch=batch, max_tokens=batch * prompt_len)
     gen = torch.Generator().manual_seed(seed)
     prompt = torch.randint(0, cfg.vocab_size, (batch, prompt_len), generator=gen)
     times = []
-    for rep in range(2):  # rep 0 warms up (captures the per-bucket step graphs)
+    for n in (warm_tokens, new_tokens):
         cache.clear()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         engine.forward(prompt[:, :-1])
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        toks = engine.generate(prompt[:, -1:], new_tokens)
+        toks = engine.generate(prompt[:, -1:], n) if n > 0 else None
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         times.append((t1 - t0, t2 - t1))
@@ -403,8 +409,10 @@ def main():
     from lokahi_amd.llama import LLAMA3_8B
 
     cfg = LLAMA3_8B
-    K = args.steps + 1  # tokens per timed generate call
-    prefill_s, decode_s, _ = run_decode(cfg, args.prompt, K, seed=1234)
+    K, W = args.steps, args.warmup  # timed and untimed decode steps (one token each)
+    if K < 1:
+        raise SystemExit("--steps must be at least 1")
+    prefill_s, decode_s, _ = run_decode(cfg, args.prompt, K, seed=1234, warm_tokens=W)
     tok_s = K / decode_s
     ms_per_step = 1e3 * decode_s / K
     token_bytes = decode_bytes(cfg, args.prompt + K // 2)
@@ -413,7 +421,7 @@ def main():
     line = {
         "metric": "decode tok/s, Llama-3-8B-shape q4 bs=1; q4 GEMV HBM GB/s (% of peak)",
         "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": K,
-        "warmup": K, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "warmup": W, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16 activations, q4 weights, fp32 accumulate",
         "data": "synthetic (random-init weights N(0,0.02) quantized on device; uniform-random prompt ids)",
         "config": {"workload": "llama3-8b-shape q4 greedy decode, batch 1, after 2048-token prefill "

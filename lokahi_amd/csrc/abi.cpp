@@ -28,8 +28,17 @@ int strata_set_error(int code, const char* fmt, ...) {
   return code;
 }
 
-int strata_ctx_scratch(strata_ctx* ctx, size_t bytes, void** out) {
+int strata_ctx_scratch(strata_ctx* ctx, size_t bytes, void** out, void* stream) {
   if (bytes > ctx->scratch_bytes) {
+    // Growing synchronizes the device and frees the old arena: neither is
+    // legal while a stream is being captured, and a graph captured earlier
+    // would keep the freed address.  Capturing callers size the arena first.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(as_stream(stream), &cs) == hipSuccess &&
+        cs != hipStreamCaptureStatusNone)
+      return strata_set_error(STRATA_EINVAL,
+                              "scratch arena must grow to %zu bytes during stream capture; "
+                              "run the call once uncaptured first", bytes);
     if (ctx->scratch) {
       // The arena may still be read by queued work on any stream.
       STRATA_HIP_CHECK(hipDeviceSynchronize());
@@ -176,9 +185,7 @@ int strata_attn_gqa(strata_ctx* ctx, const void* q, int q_dtype, const void* k, 
   if (Lq == 0) return STRATA_OK;
   STRATA_REQUIRE(q && out, "null tensor pointer");
   if (Lk == 0) {  // no keys: wv = 0 and s = 0, so out = 0 / eps = 0 (mlx_ops.py:146-147)
-    STRATA_HIP_CHECK(hipMemsetAsync(out, 0, (size_t)B * Hq * Lq * D * dtype_size(q_dtype),
-                                    as_stream(stream)));
-    return STRATA_OK;
+    return strata_zero_fill_launch(out, (int64_t)B * Hq * Lq * D * dtype_size(q_dtype), stream);
   }
   STRATA_REQUIRE(k && v, "null tensor pointer");
   return strata_attention_dispatch(ctx, q, q_dtype, k, k_dtype, v, v_dtype, kv_batch_stride,
@@ -369,7 +376,7 @@ int strata_argmax(strata_ctx* ctx, const float* logits, int64_t rows, int64_t V,
   STRATA_REQUIRE(ctx && logits && out && rows >= 0 && V > 0 && V <= INT32_MAX, "invalid arguments");
   if (rows == 0) return STRATA_OK;
   void* part = nullptr;
-  const int rc = strata_ctx_scratch(ctx, (size_t)rows * kArgmaxBlocks * 8, &part);
+  const int rc = strata_ctx_scratch(ctx, (size_t)rows * kArgmaxBlocks * 8, &part, stream);
   if (rc) return rc;
   return strata_argmax_launch(logits, rows, V, 1.0f, out, part, stream);
 }

@@ -920,7 +920,7 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
       part = ex.part;
     } else {
       void* p = nullptr;
-      const int rc = strata_ctx_scratch(ctx, (size_t)B * Hq * part_stride(nsplit, D) * sizeof(float), &p);
+      const int rc = strata_ctx_scratch(ctx, (size_t)B * Hq * part_stride(nsplit, D) * sizeof(float), &p, stream);
       if (rc) return rc;
       part = reinterpret_cast<float*>(p);
     }

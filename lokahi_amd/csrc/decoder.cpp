@@ -41,6 +41,7 @@ struct strata_decoder {
   void *h, *xn, *q, *k, *v, *qr, *attn, *o, *gate, *up, *act, *delta, *hn;
   float* logits;          // fp32 [max_batch, vocab]
   int32_t* ids;           // [max_batch] current input ids of a decode step
+  int32_t* tokens;        // [max_batch][Lmax] generated ids, copied out per call
   int* counters;          // {step, position, key count}
   float* part;            // split-K partials for graph-mode decode attention
   int part_splits;
@@ -51,11 +52,11 @@ struct strata_decoder {
   // Captured decode steps, one per key-capacity bucket: a step at key count
   // n replays the graph captured for capacity roundup(n, kKeyBucket), so the
   // split-K attention launch is sized to the context actually in use.
+  // The captured steps write into `tokens` (stride Lmax), so they stay valid
+  // for every call with the same batch and temperature.
   std::map<int, hipGraphExec_t> graphs;
   int graph_batch;
   float graph_temp;
-  int32_t* graph_out;
-  int graph_out_stride;
 };
 
 namespace {
@@ -270,6 +271,7 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
       {&d->hn, T * H * 2},
       {reinterpret_cast<void**>(&d->logits), (size_t)max_batch * c.vocab_size * 4},
       {reinterpret_cast<void**>(&d->ids), (size_t)max_batch * 4},
+      {reinterpret_cast<void**>(&d->tokens), (size_t)max_batch * kv->Lmax * 4},
       {reinterpret_cast<void**>(&d->counters), 16},
       {&d->amax, (size_t)max_batch * kArgmaxBlocks * 8},
       {reinterpret_cast<void**>(&d->rope_table), (size_t)kv->Lmax * (c.head_dim / 2) * 8},
@@ -299,7 +301,7 @@ int strata_decoder_destroy(strata_decoder* d) {
   hipDeviceSynchronize();
   for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
   void* ptrs[] = {d->h, d->xn, d->q, d->k, d->v, d->qr, d->attn, d->o, d->gate, d->up, d->act,
-                  d->delta, d->hn, d->logits, d->ids, d->counters, d->part, d->amax,
+                  d->delta, d->hn, d->logits, d->ids, d->tokens, d->counters, d->part, d->amax,
                   d->rope_table, d->rope_cur};
   for (void* p : ptrs)
     if (p) hipFree(p);
@@ -352,38 +354,43 @@ int strata_decoder_generate(strata_decoder* d, const int32_t* prompt, int B, int
   // order the decoder stream after the caller's work
   hipEvent_t ev;
   STRATA_HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
-  STRATA_HIP_CHECK(hipEventRecord(ev, as_stream(stream)));
-  STRATA_HIP_CHECK(hipStreamWaitEvent(s, ev, 0));
-  // prefill
-  RC(strata_embed_launch(d->embed, c.vocab_size, c.hidden_size, prompt, (int64_t)B * L, d->h, s));
-  RC(forward_layers(d, B, L, pos0, s));
-  RC(strata_argmax_launch(d->logits, B, c.vocab_size, temperature, d->ids, d->amax, s));
-  // counters {step, position, key count}: the advance below records token 0
-  // and leaves {1, pos0+L, pos0+L+1}, i.e. the next step processes the token
-  // at position pos0+L against pos0+L+1 keys.
-  const int init[4] = {0, pos0 + L - 1, pos0 + L, 0};
-  STRATA_HIP_CHECK(hipMemcpyAsync(d->counters, init, sizeof(init), hipMemcpyHostToDevice, s));
-  RC(strata_decode_advance_launch(d->ids, B, out_tokens, max_new, d->counters, d->rope_table,
-                                  d->kv->Lmax, c.head_dim / 2, d->rope_cur, s));
+  if (hipEventRecord(ev, as_stream(stream)) != hipSuccess || hipStreamWaitEvent(s, ev, 0) != hipSuccess) {
+    hipEventDestroy(ev);
+    return strata_set_error(STRATA_EHIP, "generate: ordering after the caller's stream failed");
+  }
+  // Positions whose K/V the launched work appends; on any error the cache
+  // length is set to what was launched, so host length and device contents
+  // agree.
+  int appended = pos0;
+  auto run = [&]() -> int {
+    // prefill
+    RC(strata_embed_launch(d->embed, c.vocab_size, c.hidden_size, prompt, (int64_t)B * L, d->h, s));
+    RC(forward_layers(d, B, L, pos0, s));
+    appended = pos0 + L;
+    RC(strata_argmax_launch(d->logits, B, c.vocab_size, temperature, d->ids, d->amax, s));
+    // counters {step, position, key count}: the advance below records token 0
+    // and leaves {1, pos0+L, pos0+L+1}, i.e. the next step processes the token
+    // at position pos0+L against pos0+L+1 keys.
+    const int init[4] = {0, pos0 + L - 1, pos0 + L, 0};
+    STRATA_HIP_CHECK(hipMemcpyAsync(d->counters, init, sizeof(init), hipMemcpyHostToDevice, s));
+    RC(strata_decode_advance_launch(d->ids, B, d->tokens, d->kv->Lmax, d->counters,
+                                    d->rope_table, d->kv->Lmax, c.head_dim / 2, d->rope_cur, s));
 
-  auto decode_step = [&](hipStream_t st, int key_cap) -> int {
-    RC(strata_embed_launch(d->embed, c.vocab_size, c.hidden_size, d->ids, B, d->h, st));
-    RC(forward_layers(d, B, 1, -1, st, key_cap));
-    RC(strata_argmax_launch(d->logits, B, c.vocab_size, temperature, d->ids, d->amax, st));
-    RC(strata_decode_advance_launch(d->ids, B, out_tokens, max_new, d->counters, d->rope_table,
-                                    d->kv->Lmax, c.head_dim / 2, d->rope_cur, st));
-    return STRATA_OK;
-  };
-  if (max_new > 1) {
-    const bool reuse = d->graph_batch == B && d->graph_temp == temperature &&
-                       d->graph_out == out_tokens && d->graph_out_stride == max_new;
-    if (!reuse) {
+    auto decode_step = [&](hipStream_t st, int key_cap) -> int {
+      RC(strata_embed_launch(d->embed, c.vocab_size, c.hidden_size, d->ids, B, d->h, st));
+      RC(forward_layers(d, B, 1, -1, st, key_cap));
+      RC(strata_argmax_launch(d->logits, B, c.vocab_size, temperature, d->ids, d->amax, st));
+      RC(strata_decode_advance_launch(d->ids, B, d->tokens, d->kv->Lmax, d->counters,
+                                      d->rope_table, d->kv->Lmax, c.head_dim / 2, d->rope_cur,
+                                      st));
+      return STRATA_OK;
+    };
+    const bool reuse = d->graph_batch == B && d->graph_temp == temperature;
+    if (max_new > 1 && !reuse) {
       for (auto& kvp : d->graphs) STRATA_HIP_CHECK(hipGraphExecDestroy(kvp.second));
       d->graphs.clear();
       d->graph_batch = B;
       d->graph_temp = temperature;
-      d->graph_out = out_tokens;
-      d->graph_out_stride = max_new;
     }
     for (int i = 1; i < max_new; ++i) {
       // step i feeds the token at position pos0 + L + i - 1: that many keys + 1
@@ -391,19 +398,22 @@ int strata_decoder_generate(strata_decoder* d, const int32_t* prompt, int B, int
       const int cap = std::min(d->kv->Lmax, (keys + kKeyBucket - 1) / kKeyBucket * kKeyBucket);
       if (!use_graph) {
         RC(decode_step(s, cap));
+        appended = keys;
         continue;
       }
       auto it = d->graphs.find(cap);
       if (it == d->graphs.end()) {
-        hipGraph_t g;
+        hipGraph_t g = nullptr;
         hipGraphExec_t ge = nullptr;
         STRATA_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
         const int crc = decode_step(s, cap);
         const hipError_t ce = hipStreamEndCapture(s, &g);
-        if (crc) return crc;
-        if (ce != hipSuccess)
+        if (crc || ce != hipSuccess) {
+          if (ce == hipSuccess && g) hipGraphDestroy(g);
+          if (crc) return crc;
           return strata_set_error(STRATA_EHIP, "decode graph capture failed: %s",
                                   hipGetErrorString(ce));
+        }
         const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
         hipGraphDestroy(g);
         if (ie != hipSuccess)
@@ -412,13 +422,24 @@ int strata_decoder_generate(strata_decoder* d, const int32_t* prompt, int B, int
         it = d->graphs.emplace(cap, ge).first;
       }
       STRATA_HIP_CHECK(hipGraphLaunch(it->second, s));
+      appended = keys;
     }
-  }
-  STRATA_HIP_CHECK(hipEventRecord(ev, s));
-  STRATA_HIP_CHECK(hipStreamWaitEvent(as_stream(stream), ev, 0));
-  STRATA_HIP_CHECK(hipStreamSynchronize(s));
-  STRATA_HIP_CHECK(hipEventDestroy(ev));
-  set_lengths(d, pos0 + L + max_new - 1);
+    STRATA_HIP_CHECK(hipMemcpy2DAsync(out_tokens, (size_t)max_new * 4, d->tokens,
+                                      (size_t)d->kv->Lmax * 4, (size_t)max_new * 4, B,
+                                      hipMemcpyDeviceToDevice, s));
+    return STRATA_OK;
+  };
+  const int rc = run();
+  // The caller's stream waits for everything launched, success or not.
+  const hipError_t e1 = hipEventRecord(ev, s);
+  const hipError_t e2 = e1 == hipSuccess ? hipStreamWaitEvent(as_stream(stream), ev, 0) : e1;
+  const hipError_t e3 = hipStreamSynchronize(s);
+  hipEventDestroy(ev);
+  set_lengths(d, appended);
+  if (rc) return rc;
+  if (e2 != hipSuccess || e3 != hipSuccess)
+    return strata_set_error(STRATA_EHIP, "generate: stream synchronization failed: %s",
+                            hipGetErrorString(e3 != hipSuccess ? e3 : e2));
   return STRATA_OK;
 }
 

@@ -132,6 +132,17 @@ __global__ void add_kernel(const uint16_t* __restrict__ x, const uint16_t* __res
     y[i] = f32_to_bf16(bf16_to_f32(x[i]) + bf16_to_f32(r[i]));
 }
 
+// Clears n bytes (a kernel, not hipMemsetAsync: memset nodes recorded into a
+// captured graph have given wrong results on replays after the first).
+__global__ void zero_fill_kernel(uint8_t* __restrict__ p, int64_t n) {
+  const int64_t n16 = n >> 4;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n16;
+       i += (int64_t)gridDim.x * blockDim.x)
+    reinterpret_cast<uint4*>(p)[i] = make_uint4(0, 0, 0, 0);
+  const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (t < (n & 15)) p[(n16 << 4) + t] = 0;
+}
+
 __global__ void embed_kernel(const uint16_t* __restrict__ table, int64_t V, int64_t H,
                              const int32_t* __restrict__ ids, uint16_t* __restrict__ y) {
   const int64_t t = blockIdx.x;
@@ -274,6 +285,16 @@ int strata_silu_mul_launch(const void* g, const void* u, int64_t n, void* a, voi
 int strata_add_launch(const void* x, const void* r, int64_t n, void* y, void* stream) {
   hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream),
                      (const uint16_t*)x, (const uint16_t*)r, n, (uint16_t*)y);
+  STRATA_HIP_CHECK(hipGetLastError());
+  return STRATA_OK;
+}
+
+int strata_zero_fill_launch(void* p, int64_t bytes, void* stream) {
+  if (bytes <= 0) return STRATA_OK;
+  STRATA_REQUIRE(aligned16(p), "zero fill: pointer must be 16-byte aligned");
+  const int64_t n16 = (bytes >> 4) > 0 ? (bytes >> 4) : 1;
+  hipLaunchKernelGGL(zero_fill_kernel, dim3(grid_for(n16)), dim3(256), 0, as_stream(stream),
+                     (uint8_t*)p, bytes);
   STRATA_HIP_CHECK(hipGetLastError());
   return STRATA_OK;
 }

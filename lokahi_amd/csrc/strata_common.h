@@ -141,7 +141,7 @@ struct strata_ctx {
 };
 
 // Returns a device scratch buffer of at least `bytes` (owned by ctx).
-int strata_ctx_scratch(strata_ctx* ctx, size_t bytes, void** out);
+int strata_ctx_scratch(strata_ctx* ctx, size_t bytes, void** out, void* stream);
 
 // Floats of decode split-K partials per (b, query head): o[nsplit][D] then
 // (m, s)[nsplit]; a multiple of 4 (16-byte blocks) for D % 4 == 0.

@@ -66,6 +66,8 @@ int strata_rmsnorm_launch(void* x, const void* res, const uint16_t* w, int64_t r
                           float eps, void* y, void* stream);
 int strata_silu_mul_launch(const void* g, const void* u, int64_t n, void* a, void* stream);
 int strata_add_launch(const void* x, const void* r, int64_t n, void* y, void* stream);
+// Clears `bytes` bytes at p (16-byte aligned) with a kernel.
+int strata_zero_fill_launch(void* p, int64_t bytes, void* stream);
 int strata_embed_launch(const uint16_t* table, int64_t V, int64_t H, const int32_t* ids,
                         int64_t n, void* y, void* stream);
 constexpr int kArgmaxBlocks = 128;  // workgroups per row of the first argmax stage

@@ -207,6 +207,16 @@ class HipKVCache:
         torch.cuda.current_stream(self.device).synchronize()  # kt/vt die with this frame
         del self._disk_offloaded[layer_idx]
 
+    def load_offloaded_layers(self) -> None:
+        """Restore every offloaded layer onto the device.
+
+        The native decoder appends into device memory directly; a layer left
+        on disk would later be reloaded over those appends (stale K/V, length
+        reset to the file's).  Callers that hand the cache to native code
+        call this first."""
+        for idx in sorted(self._disk_offloaded):
+            self._load_layer_from_disk(idx)
+
     def offload_layers_to_disk(self, layer_indices: Optional[List[int]] = None) -> None:
         """``mlx_kvcache.py:252-264``: all cached layers when ``layer_indices`` is None."""
         for idx in (self.in_memory_layers() if layer_indices is None else layer_indices):

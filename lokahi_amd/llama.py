@@ -259,6 +259,7 @@ class DecoderEngine:
         import ctypes as C
         from . import _abi
         from .ops import _stream
+        self.cache.load_offloaded_layers()
         ids32 = ids.to(device=self.model.device, dtype=torch.int32).contiguous()
         B, L = ids32.shape
         out = torch.empty((B, self.vocab), dtype=torch.float32, device=self.model.device)
@@ -271,10 +272,10 @@ class DecoderEngine:
                  use_graph: bool = True) -> torch.Tensor:
         from . import _abi
         from .ops import _stream
+        self.cache.load_offloaded_layers()
         ids32 = prompt.to(device=self.model.device, dtype=torch.int32).contiguous()
         B, L = ids32.shape
-        # one output buffer per (B, max_new): the native engine reuses its
-        # captured decode-step graphs only while the output address is stable
+        # one output buffer per (B, max_new), reused across calls
         key = (B, max_new)
         if key not in self._outs:
             self._outs[key] = torch.empty((B, max_new), dtype=torch.int32,

@@ -53,7 +53,14 @@ class Config:
 
 
 def rms_norm(x: np.ndarray, weight_bits: np.ndarray, eps: float) -> np.ndarray:
-    """fp32 RMSNorm of bf16-valued ``x`` (``llama_mlx.py:77-92``), rounded to bf16."""
+    """fp32 RMSNorm of bf16-valued ``x`` (``llama_mlx.py:77-92``), rounded to bf16.
+
+    Operand order follows the uncompiled branch (``llama_mlx.py:89-91``:
+    ``x * rsqrt(var + eps)`` then ``weight * x``); the compiled branch
+    (``metal_optimizations.py:96``) forms ``weight * x`` first.  The two
+    differ by at most one fp32 rounding before the bf16 rounding.  Pinned
+    against torch's fp32 ``rms_norm`` and a float64 closed form in
+    ``tests/test_oracle_pins.py``."""
     x = np.asarray(x, dtype=np.float32)
     var = np.mean(x.astype(np.float64) ** 2, axis=-1, keepdims=True)
     r = (1.0 / np.sqrt(var + eps)).astype(np.float32)
@@ -64,7 +71,8 @@ def rms_norm(x: np.ndarray, weight_bits: np.ndarray, eps: float) -> np.ndarray:
 def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     """``silu(g) * u`` in fp32, rounded to bf16 (``llama_mlx.py:399-407``)."""
     g = g.astype(np.float64)
-    return round_bf16((g / (1.0 + np.exp(-g)) * u).astype(np.float32))
+    with np.errstate(over="ignore"):  # exp(-g) = inf for g << 0 gives silu = -0
+        return round_bf16((g / (1.0 + np.exp(-g)) * u).astype(np.float32))
 
 
 class OracleLlama:

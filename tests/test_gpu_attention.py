@@ -96,7 +96,8 @@ def _c_decode(q, k, v):
     return out.reshape(B, Hq, 1, D)
 
 
-@pytest.mark.parametrize("B,L", [(1, 1024), (1, 8192), (16, 1024), (1, 32768), (16, 8192)])
+@pytest.mark.parametrize("B,L", [(1, 1024), (1, 8192), (16, 1024), (1, 32768), (16, 8192),
+                                 (16, 32768)])
 def test_config3_cached_decode_bf16(dev, B, L):
     """Hq32/Hkv8, D128, bf16 KV cache; append one token, then attend."""
     from types import SimpleNamespace

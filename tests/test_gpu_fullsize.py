@@ -51,3 +51,35 @@ def test_config5_gate_gemm_8k_library_and_fused_paths(dev, monkeypatch):
     rows = np.array([0, 1, 255, 256, 4097, 8191])
     ref = q4.quantized_matmul(bf16_bits_to_f32(x[rows]), w, s, b)
     assert rel_err(to_np_f32(lib)[rows], ref) < TOL_BF16
+
+
+@pytest.mark.parametrize("name,N,K", [("q/o", 4096, 4096), ("k/v", 1024, 4096),
+                                      ("up", 14336, 4096), ("down", 4096, 14336)])
+def test_config5_layer_gemms_8k_sampled_rows(dev, name, N, K):
+    """Every config-5 linear shape at M = 8192 on the default prefill path;
+    rows at tile edges against the float64 oracle, plus linearity in x."""
+    from lokahi_amd import ops
+    from tests.gpu_util import bits
+    M = 8192
+    g = torch.Generator(device=dev).manual_seed(N * 7 + K)
+    tw, ts, tb = ops.quantize(torch.randn((N, K), generator=g, device=dev) * 0.02)
+    tx = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    y = ops.linear(tx, tw, ts, tb, out_dtype=torch.float32)
+    w, s, b = bits(tw), bits(ts), bits(tb)
+    rows = np.array([0, 1, 127, 128, 255, 256, 4097, 8190, 8191])
+    xr = bf16_bits_to_f32(bits(tx[torch.from_numpy(rows).to(dev)]))
+    ref = q4.quantized_matmul(xr, w, s, b)
+    assert rel_err(to_np_f32(y)[rows], ref) < TOL_BF16, name
+    # the MFMA path stages each dequantized weight as bf16 (one RNE rounding of
+    # s*q + b, as MLX's qmm stages tiles in the activation dtype): against that
+    # matrix the fp32 tolerance holds
+    from oracle.bf16 import round_bf16
+    wq = round_bf16(q4.dequantize(w, s, b, 64).astype(np.float32)).astype(np.float64)
+    ref16 = xr.astype(np.float64) @ wq.T
+    assert rel_err(to_np_f32(y)[rows], ref16) < TOL_F32, name
+    # bf16 output path and linearity: y(2x) == 2 y(x) exactly (power-of-two scale)
+    y2 = ops.linear(tx * 2, tw, ts, tb, out_dtype=torch.float32)
+    assert torch.equal(y2, 2 * y)
+    yb = ops.linear(tx, tw, ts, tb)
+    assert yb.dtype == torch.bfloat16
+    assert rel_err(to_np_f32(yb)[rows], ref) < TOL_BF16

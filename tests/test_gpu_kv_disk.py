@@ -92,3 +92,35 @@ def test_disk_cache_keeps_at_most_n_layers_in_memory(dev, tmp_path):
         assert cache.in_memory_layers() == [layer]
     assert len(cache) == 3 and sorted(cache._disk_offloaded) == [0, 1]
     assert torch.equal(cache[0]["key"], _states(0, 2, dev)[0])
+
+
+def test_engine_reloads_offloaded_layers_before_appending(dev, tmp_path):
+    """The native engine appends into device memory: layers offloaded to disk
+    are restored first, so no later access reloads a stale file over them."""
+    from oracle import llama as oll
+    from lokahi_amd.kvcache import HipKVCache
+    from lokahi_amd.llama import HipLlamaForCausalLM, LlamaConfig, weights_to_device
+    cfg = oll.Config(vocab_size=128, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                     num_attention_heads=2, num_key_value_heads=1, rope_theta=10000.0)
+    hw = oll.random_weights(cfg, seed=5, std=0.05)
+    lc = LlamaConfig(**{f: getattr(cfg, f) for f in cfg.__dataclass_fields__})
+    model = HipLlamaForCausalLM(lc, weights_to_device(hw, dev))
+    prompt = torch.tensor([[3, 9, 27, 81, 115]])
+
+    ref_cache = model.new_cache(1, 32)
+    ref_tokens = model.generate(prompt[:, :3], max_new_tokens=1, past_key_values=ref_cache)
+    ref_tokens = model.generate(prompt[:, 3:], max_new_tokens=6, past_key_values=ref_cache)
+
+    cache = HipKVCache(cfg, str(tmp_path), max_length=32, dtype=torch.bfloat16)
+    model.generate(prompt[:, :3], max_new_tokens=1, past_key_values=cache)
+    cache.offload_layers_to_disk()
+    assert cache.in_memory_layers() == []
+    got = model.generate(prompt[:, 3:], max_new_tokens=6, past_key_values=cache)
+    assert torch.equal(got, ref_tokens)
+    want = ref_cache.get_seq_length()
+    assert want == 3 + 2 + 5
+    for li in range(cfg.num_hidden_layers):
+        assert cache.get_seq_length(li) == want  # no reload cuts the engine's appends off
+        k, v = cache.views(li)
+        rk, rv = ref_cache.views(li)
+        assert torch.equal(k, rk) and torch.equal(v, rv)
