@@ -46,14 +46,14 @@ def test_config4_full_28_layers_prompt_2048_plus_256_tokens(dev):
     gen = torch.Generator().manual_seed(77)
     prompt = torch.randint(0, cfg.vocab_size, (1, 2048), generator=gen)
     cache = model.new_cache(1, 2048 + 256 + 8)
-    eng = DecoderEngine(model, cache, max_batch=1, max_tokens=2048)
+    eng = DecoderEngine(model, cache, max_batch=1, max_tokens=2048 + 32)
 
     graph = eng.generate(prompt, 256, use_graph=True)
     assert cache.get_seq_length() == 2048 + 255
     cache.clear()
     host = eng.generate(prompt, 256, use_graph=False)
     assert torch.equal(graph, host)
-    assert graph.shape == (1, 2304) and torch.equal(graph[:, :2048], prompt)
+    assert graph.shape == (1, 2304) and torch.equal(graph[:, :2048].cpu(), prompt)
 
     # engine logits == op-by-op driver logits, after the prompt and after 32 tokens
     seq = graph[:, :2048 + 32]

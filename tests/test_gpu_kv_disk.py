@@ -104,7 +104,7 @@ def test_engine_reloads_offloaded_layers_before_appending(dev, tmp_path):
                      num_attention_heads=2, num_key_value_heads=1, rope_theta=10000.0)
     hw = oll.random_weights(cfg, seed=5, std=0.05)
     lc = LlamaConfig(**{f: getattr(cfg, f) for f in cfg.__dataclass_fields__})
-    model = HipLlamaForCausalLM(lc, weights_to_device(hw, dev))
+    model = HipLlamaForCausalLM(lc, weights_to_device(hw))
     prompt = torch.tensor([[3, 9, 27, 81, 115]])
 
     ref_cache = model.new_cache(1, 32)
