@@ -127,6 +127,20 @@ int strata_attn_gqa(strata_ctx* ctx, const void* q, int q_dtype, const void* k, 
                     int Lq, int Lk, int D, int causal, int q_blk, int k_blk, float eps,
                     void* out, void* stream);
 
+/* No counterpart in the reference.  strata_attn_gqa for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): same arguments, results and errors, but
+ * the split-K partials live in a static 16 MiB device array instead of the
+ * ctx arena, and nothing is allocated.  Decode shapes needing more partials
+ * (B * Hq * splits * (D + 4) * 4 bytes) fail with STRATA_EINVAL.  Every call
+ * on one GPU shares that array: calls that overlap on one GPU (concurrent
+ * streams or threads) race. */
+int strata_attn_gqa_noalloc(strata_ctx* ctx, const void* q, int q_dtype, const void* k,
+                            int k_dtype, const void* v, int v_dtype, int64_t kv_batch_stride,
+                            int64_t kv_head_stride, const int32_t* qpos, int B, int Hq, int Hkv,
+                            int Lq, int Lk, int D, int causal, int q_blk, int k_blk, float eps,
+                            void* out, void* stream);
+
 /* ---------------------------------------------------------------- KV cache
  * Replaces MLXKVCache's append/read contract (src/ollm/mlx_kvcache.py:65-172):
  * per-layer K/V [B,Hkv,Lmax,D] buffers, per-layer lengths, and rejection of

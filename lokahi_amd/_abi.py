@@ -71,6 +71,10 @@ _SIGS = {
                          C.c_int, C.c_int64, C.c_int64, C.c_void_p, C.c_int, C.c_int, C.c_int,
                          C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                          C.c_void_p, C.c_void_p], C.c_int),
+    "strata_attn_gqa_noalloc": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
+                                 C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_void_p, C.c_int,
+                                 C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                 C.c_int, C.c_float, C.c_void_p, C.c_void_p], C.c_int),
     "strata_kv_create": ([C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                           C.c_void_p, C.c_void_p, c_void_pp], C.c_int),
     "strata_kv_destroy": ([C.c_void_p], C.c_int),

@@ -18,6 +18,13 @@ namespace {
 thread_local std::string g_error;
 }  // namespace
 
+// Scratch of strata_attn_gqa_noalloc: a file-scope device array, so that
+// entry point never allocates.  Each device holds its own copy until the
+// process ends; host code reaches it only through the address
+// hipGetSymbolAddress returns for the current device (kept in the ctx).
+constexpr size_t kFixedScratchBytes = 16u << 20;
+static __device__ __align__(256) float scratch[kFixedScratchBytes / sizeof(float)];
+
 int strata_set_error(int code, const char* fmt, ...) {
   char buf[1024];
   va_list ap;
@@ -80,6 +87,16 @@ int strata_ctx_create(int device, strata_ctx** out) {
   c->max_lds_per_block = 65536;  // portable launch limit for dynamic LDS
   c->scratch = nullptr;
   c->scratch_bytes = 0;
+  c->fixed_scratch = nullptr;
+  // With `dev` current: this device's address of the static scratch array.
+  void* fixed = nullptr;
+  const hipError_t se = hipGetSymbolAddress(&fixed, HIP_SYMBOL(scratch));
+  if (se != hipSuccess || fixed == nullptr) {
+    delete c;
+    return strata_set_error(STRATA_EHIP, "hipGetSymbolAddress(scratch) failed: %s",
+                            hipGetErrorString(se));
+  }
+  c->fixed_scratch = static_cast<float*>(fixed);
   *out = c;
   return STRATA_OK;
 }
@@ -191,6 +208,44 @@ int strata_attn_gqa(strata_ctx* ctx, const void* q, int q_dtype, const void* k, 
   return strata_attention_dispatch(ctx, q, q_dtype, k, k_dtype, v, v_dtype, kv_batch_stride,
                                    kv_head_stride, qpos, B, Hq, Hkv, Lq, Lk, D, causal, eps, out,
                                    AttnExtra{}, stream);
+}
+
+int strata_attn_gqa_noalloc(strata_ctx* ctx, const void* q, int q_dtype, const void* k,
+                            int k_dtype, const void* v, int v_dtype, int64_t kv_batch_stride,
+                            int64_t kv_head_stride, const int32_t* qpos, int B, int Hq, int Hkv,
+                            int Lq, int Lk, int D, int causal, int q_blk, int k_blk, float eps,
+                            void* out, void* stream) {
+  STRATA_REQUIRE(ctx != nullptr, "ctx is NULL");
+  STRATA_REQUIRE(ctx->fixed_scratch != nullptr, "ctx has no static scratch address");
+  STRATA_REQUIRE(q_blk > 0 && k_blk > 0, "attention block sizes must be positive");
+  STRATA_REQUIRE(dtype_ok(q_dtype) && dtype_ok(k_dtype) && dtype_ok(v_dtype), "unknown dtype code");
+  STRATA_REQUIRE(B > 0 && Lq >= 0 && Lk >= 0 && D > 0, "invalid shape");
+  STRATA_REQUIRE(D <= 256, "head_dim %d > 256 is not supported", D);
+  STRATA_REQUIRE(Hkv > 0 && Hq % Hkv == 0, "query heads must be divisible by key/value heads");
+  STRATA_REQUIRE(!causal || Lk >= Lq, "causal attention requires key length >= query length");
+  STRATA_REQUIRE(kv_head_stride >= (int64_t)Lk * D && kv_batch_stride >= kv_head_stride * Hkv,
+                 "key/value strides are smaller than the key/value extent");
+  if (Lq == 0) return STRATA_OK;
+  STRATA_REQUIRE(q && out, "null tensor pointer");
+  if (Lk == 0)
+    return strata_zero_fill_launch(out, (int64_t)B * Hq * Lq * D * dtype_size(q_dtype), stream);
+  STRATA_REQUIRE(k && v, "null tensor pointer");
+  // Only the split-K decode uses scratch (its partials, each written before
+  // it is read, so nothing needs clearing).
+  AttnExtra ex{};
+  if (Lq == 1) {
+    const int splits = strata_attn_decode_splits(ctx, B, Hkv, Lk);
+    const size_t need = splits > 1 ? (size_t)B * Hq * part_stride(splits, D) * sizeof(float) : 0;
+    STRATA_REQUIRE(need <= kFixedScratchBytes,
+                   "attn_gqa_noalloc: %d x %d query heads over %d keys need %zu bytes of split-K "
+                   "scratch; the static scratch holds %zu",
+                   B, Hq, Lk, need, kFixedScratchBytes);
+    ex.part = ctx->fixed_scratch;
+    ex.part_splits = splits;
+  }
+  return strata_attention_dispatch(ctx, q, q_dtype, k, k_dtype, v, v_dtype, kv_batch_stride,
+                                   kv_head_stride, qpos, B, Hq, Hkv, Lq, Lk, D, causal, eps, out,
+                                   ex, stream);
 }
 
 // ---------------------------------------------------------------- KV cache

@@ -138,6 +138,7 @@ struct strata_ctx {
   void* scratch;        // device scratch arena (split-K partials), grown on demand
   size_t scratch_bytes;
   struct GemmLt* lt;    // prefill GEMM state (library handle, plans, bf16 weight tile)
+  float* fixed_scratch; // this device's copy of the library's static scratch array
 };
 
 // Returns a device scratch buffer of at least `bytes` (owned by ctx).
