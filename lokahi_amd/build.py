@@ -31,12 +31,20 @@ COMMON = [
 ]
 
 
+# Per-file flags.  The prefill GEMM keeps its staging arrays in registers:
+# LLVM would otherwise move them to LDS (promote-alloca), which turns every
+# prefetch into a load-then-wait.
+FILE_FLAGS = {
+    "q4_gemm_mfma.hip": ["-mllvm", "-disable-promote-alloca-to-lds"],
+}
+
+
 def sources():
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)

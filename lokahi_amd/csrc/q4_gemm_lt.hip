@@ -76,13 +76,6 @@ struct GemmLt {
 
 namespace {
 
-// Read per call (a prefill GEMM runs for tens of microseconds at least), so a
-// process can switch paths; 0 or a negative value disables the library path.
-int lt_min_rows() {
-  const char* e = std::getenv("STRATA_GEMM_LT_MIN_M");
-  return e ? std::atoi(e) : 256;
-}
-
 #define LT_CHECK(expr)                                                              \
   do {                                                                              \
     hipblasStatus_t _s = (expr);                                                    \
@@ -194,9 +187,25 @@ void strata_gemm_lt_destroy(strata_ctx* ctx) {
 int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t* w,
                    const uint16_t* s, const uint16_t* b, int N, void* y, int y_dtype,
                    void* stream) {
-  const int min_rows = lt_min_rows();
-  if (min_rows <= 0 || M < min_rows || !aligned16(y))
+  // Default: the hand-written kernels only (fused dequant, bf16 MFMA).
+  // STRATA_GEMM_LT_MIN_M > 0 opts into the dequantize + hipBLASLt path from
+  // that many rows (comparison runs only).
+  const char* e = getenv("STRATA_GEMM_LT_MIN_M");
+  const int min_rows = e ? atoi(e) : 0;
+  if (min_rows <= 0 || M < min_rows || !aligned16(y)) {
+    // Full 256-row tiles on the 256 x 256 kernel, remaining rows (and any N
+    // that is not a multiple of 256) on the 128 x 128 kernel.
+    const int Mf = M / 256 * 256;
+    if (Mf >= kMfmaMinRows && N % 256 == 0) {
+      int rc = strata_q4_gemm_mfma_launch(x, Mf, K, w, s, b, N, y, y_dtype, stream);
+      if (rc || Mf == M) return rc;
+      const size_t ye = y_dtype == STRATA_BF16 ? 2 : 4;
+      return strata_q4_gemm_launch(static_cast<const uint16_t*>(x) + (size_t)Mf * K, M - Mf, K,
+                                   w, s, b, N, static_cast<char*>(y) + (size_t)Mf * N * ye,
+                                   y_dtype, stream);
+    }
     return strata_q4_gemm_launch(x, M, K, w, s, b, N, y, y_dtype, stream);
+  }
   int rc = lt_init(ctx);
   if (rc) return rc;
   GemmLt* lt = ctx->lt;

@@ -1,0 +1,373 @@
+// Prefill q4 GEMM for large M: Y[M, N] = X[M, K] @ dequant(W)[N, K]^T on
+// bf16 MFMA, dequantizing in the kernel (no bf16 copy of the weight).
+//
+// Same maths as mx.quantized_matmul(transpose=True) on the prefill path
+// (src/ollm/llama_mlx.py:53-74, 393-432): W[n, k] = s[n, k/64] * q + b[n, k/64],
+// rounded once to bf16 (fp32 FMA, round-to-nearest-even), as MLX's qmm
+// stages dequantized tiles in the activation dtype; fp32 accumulation.
+//
+// Workgroup tile 256 (M) x 256 (N), K step 64 = one quantization group.
+// 4 waves, one per SIMD: wave w owns all 256 rows x columns 64w .. 64w+63,
+// i.e. 16 x 4 blocks of v_mfma_f32_16x16x32_bf16 (256 fp32 accumulators per
+// lane, in AGPRs).
+//   * X tiles go through LDS: 256 x 64 bf16 (32 KB) per stage, 16-byte
+//     chunks XOR-swizzled (chunk c of row r at c ^ ((r >> 1) & 7)) so the
+//     MFMA operand reads of a 16-lane phase touch 64 distinct banks.
+//   * Weights are dequantized in registers, straight into the B operand:
+//     16x16x32 wants, per lane, 8 consecutive k of one weight row = one
+//     packed uint32 word, so each wave handles exactly the words of its own
+//     64 columns; each weight is dequantized once per workgroup (mask,
+//     v_cvt_f32_ubyteN, FMA, v_cvt_pk_bf16_f32).
+//   * Every global read is a direct global -> LDS buffer load (no VGPR
+//     staging): the X tile, and each wave's own weight words, scales and
+//     biases.  Three LDS stages; the loads of step g+2 are issued at the
+//     top of step g, so they have ~1.5 steps to land.
+//   * While the MFMAs of step g run, the wave dequantizes the fragments the
+//     next MFMAs need (each k half is rewritten right after its last MFMA
+//     of the step has issued), in fixed slots between the MFMAs.  One
+//     barrier per K step.
+//   * Workgroup order: tiles are dealt to the 8 XCDs in contiguous runs
+//     (block b runs on XCD b % 8), grouped 4 M-tiles x N-tiles, so the
+//     ~32 workgroups resident on one XCD share X and W tiles in its L2.
+#include <type_traits>
+
+#include "strata_common.h"
+
+namespace {
+
+constexpr int TM = 256, TN = 256, TK = 64;
+constexpr int NTHR = 256;
+constexpr int WN = 64;              // columns per wave
+constexpr int MB = TM / 32;         // 32-row MFMA blocks per wave
+constexpr int NB = WN / 32;         // 32-column MFMA blocks per wave
+constexpr int KB = TK / 16;         // 16-deep MFMA k blocks per K step
+constexpr int XCH = TM * 8 / NTHR;  // X chunks (16 B) staged per thread per K step
+constexpr int kGroupM = 4;          // M tiles per group of the tile order
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer descriptor, gfx9 data format
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// 32x32x16 rather than 16x16x32: each instruction runs long enough for the
+// VALU dequantization issued between MFMAs to overlap it (measured on
+// MI355X: 2 VALU per 16x16x32 cost a third of the MFMA rate, 4 per
+// 32x32x16 about 14%).
+__device__ __forceinline__ f32x16_t mfma32(const uint4& a, const uint4& b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+template <int B>
+__device__ __forceinline__ float ubyte(uint32_t v) {
+  float r;
+  if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+  if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+  if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+  if constexpr (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
+// 8 codes of one word -> 8 bf16 (s*q + b, fp32 FMA then RNE), k order.
+__device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float b) {
+  const uint32_t lo = w & 0x0f0f0f0fu;         // codes 0, 2, 4, 6
+  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;  // codes 1, 3, 5, 7
+  uint4 o;
+  o.x = pk_bf16(fmaf(s, ubyte<0>(lo), b), fmaf(s, ubyte<0>(hi), b));
+  o.y = pk_bf16(fmaf(s, ubyte<1>(lo), b), fmaf(s, ubyte<1>(hi), b));
+  o.z = pk_bf16(fmaf(s, ubyte<2>(lo), b), fmaf(s, ubyte<2>(hi), b));
+  o.w = pk_bf16(fmaf(s, ubyte<3>(lo), b), fmaf(s, ubyte<3>(hi), b));
+  return o;
+}
+
+// Tile index -> (m tile, n tile): XCD-contiguous runs, then groups of
+// kGroupM M tiles sweeping the N tiles.
+__device__ __forceinline__ void tile_of(int b, int mt, int nt, int* tm, int* tn) {
+  const int total = mt * nt;
+  int t = b;
+  if (total % 8 == 0) t = (b % 8) * (total / 8) + b / 8;
+  const int per_group = kGroupM * nt;
+  const int grp = t / per_group, rem = t - grp * per_group;
+  const int gm = min(kGroupM, mt - grp * kGroupM);
+  *tm = grp * kGroupM + rem % gm;
+  *tn = rem / gm;
+}
+
+typedef int v4i32_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor (wave-uniform) for `bytes` bytes at p.
+__device__ __forceinline__ v4i32_t rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  v4i32_t r = {(int)(uint32_t)a, (int)((a >> 32) & 0xffffu), (int)bytes, kRsrcWord3};
+  r.x = __builtin_amdgcn_readfirstlane(r.x);
+  r.y = __builtin_amdgcn_readfirstlane(r.y);
+  return r;
+}
+
+// Direct global -> LDS loads (buffer_load ... lds): lane l of the wave writes
+// its 16 bytes at LDS byte address lds + 16 l (2-byte loads: zero-extended
+// to 4 bytes at lds + 4 l).  Issued as inline
+// assembly: the compiler does not track them, so it inserts no waits for
+// them; the kernel waits with explicit s_waitcnt vmcnt.
+__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, v4i32_t r, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+__device__ __forceinline__ void dma2(uint32_t lds, uint32_t voff, v4i32_t r, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_ushort %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+
+// LDS stage layout (bytes): X tile 256 x 128 (swizzled 16-byte chunks), then
+// per wave its 64 weight rows x 32 bytes, then per wave 64 scales and 64
+// biases (a 2-byte load lands zero-extended in 4 bytes of LDS).  Three
+// stages: the loads of step g + 2 are issued at the top of step g.
+constexpr int kXBytes = TM * TK * 2;             // 32 KB
+constexpr int kWBytes = 4 * 64 * 32;             // 8 KB
+constexpr int kSBBytes = 4 * 64 * 4 * 2;         // 2 KB
+constexpr int kStage = kXBytes + kWBytes + kSBBytes;
+constexpr int kStages = 3;
+constexpr int kDmaPerStep = XCH + 2 + 1 + 1;     // per lane: X chunks, W halves, s, b
+
+// Full tiles only: M % 256 == 0, N % 256 == 0, K % 64 == 0, and every
+// operand under 4 GiB (the launcher checks).
+template <typename YT>
+__global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
+                         const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
+                         const uint16_t* __restrict__ bi, int N, YT* __restrict__ y) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int mt = M / TM, nt = N / TN;
+  int tmi, tni;
+  tile_of(blockIdx.x, mt, nt, &tmi, &tni);
+  const int m0 = tmi * TM, n0 = tni * TN;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = K / TK;
+  const uint32_t kb = (uint32_t)K * 2;   // bytes per X row
+  const uint32_t wb = (uint32_t)K / 2;   // bytes per weight row
+  const uint32_t gb = (uint32_t)G * 2;   // bytes per scale row
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) uint8_t*)lds);
+
+  const v4i32_t rx = rsrc(x, (uint32_t)((size_t)M * kb));
+  const v4i32_t rw = rsrc(w, (uint32_t)((size_t)N * wb));
+  const v4i32_t rs = rsrc(sc, (uint32_t)((size_t)N * gb));
+  const v4i32_t rb = rsrc(bi, (uint32_t)((size_t)N * gb));
+
+  // X DMA instruction i of wave w fills 16-byte slots S = (8w + i) * 64 + lane
+  // of the stage: row r = S / 8, slot p = lane % 8 holds chunk
+  // c = p ^ ((r >> 1) & 7) = (lane & 7) ^ (4 (i & 1) + (lane >> 4)).
+  const uint32_t xl0 = (lane >> 3) * kb + (((lane & 7) ^ (lane >> 4)) << 4);
+  const uint32_t xl1 = (lane >> 3) * kb + (((lane & 7) ^ (4 + (lane >> 4))) << 4);
+  // W DMA j of this wave: 16-byte chunk q = 64 j + lane = row q/2, half q%2.
+  const uint32_t wl = (lane >> 1) * wb + (lane & 1) * 16;
+  const uint32_t sl = lane * gb;
+  // DMA piece p (0 .. kDmaPerStep - 1) of step g into stage stg: X chunks
+  // 0-7, the two weight halves, the scales, the biases.
+  auto issue1 = [&](int g, int stg, int p) {
+    const uint32_t base = lds0 + stg * kStage;
+    if (p < XCH) {
+      dma16(base + (wave * XCH + p) * 1024, (p & 1) ? xl1 : xl0, rx,
+            (uint32_t)(m0 + (wave * XCH + p) * 8) * kb + g * TK * 2);
+    } else if (p < XCH + 2) {
+      const int j = p - XCH;
+      dma16(base + kXBytes + wave * 2048 + j * 1024, wl, rw,
+            (uint32_t)(n0 + wave * WN + j * 32) * wb + g * 32);
+    } else {
+      const int h = p - XCH - 2;  // 0: scales, 1: biases
+      dma2(base + kXBytes + kWBytes + wave * 512 + h * 256, sl, h ? rb : rs,
+           (uint32_t)(n0 + wave * WN) * gb + g * 2);
+    }
+  };
+  auto issue = [&](int g, int stg) {
+#pragma unroll
+    for (int p = 0; p < kDmaPerStep; ++p) issue1(g, stg, p);
+  };
+  // Wait until at most N loads are outstanding (loads complete in order).
+  auto vm_wait = [&](auto N) {
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(decltype(N)::value) : "memory");
+  };
+  auto vm_wait_step = [&]() { vm_wait(std::integral_constant<int, kDmaPerStep>{}); };
+
+  // 32x32x16 operand layouts (wave64): A (32 x 16): lane l holds row l % 32,
+  // k 8 (l / 32) .. +8; B (16 x 32): lane l holds column l % 32, the same k;
+  // C (32 x 32): lane l holds column l % 32, rows 8 (i / 4) + 4 (l / 32) +
+  // i % 4 for i < 16.
+  const int c32 = lane & 31, kh = lane >> 5;
+  // A fragment (mb, kblk): row mb*32 + c32, 16-byte chunk 2 kblk + kh of the
+  // swizzled row ((r >> 1) & 7 == (c32 >> 1) & 7 for every mb).
+  auto aoff = [&](int mb, int kblk) {
+    return ((mb * 32 + c32) * TK + (((2 * kblk + kh) ^ ((c32 >> 1) & 7)) << 3)) * 2;
+  };
+
+  // B fragment (nb, kblk) = 8 codes of row nb*32 + c32, word 2 kblk + kh of
+  // the group.  bf[nb][kblk]: frag (nb, k) of step g is rewritten for step
+  // g + 1 in the k block after its last use (k block 3 of step g + 1 during
+  // k block 0 of step g + 1).
+  uint4 bf[NB][KB];
+  uint32_t dw[NB];
+  float dsf[NB], dbf[NB];
+  auto read_sb = [&](int stg, bool live) {
+    const uint8_t* ss = lds + stg * kStage + kXBytes + kWBytes + wave * 512;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int row = nb * 32 + c32;
+      dsf[nb] = live ? bf16_to_f32(*reinterpret_cast<const uint16_t*>(ss + row * 4)) : 0.f;
+      dbf[nb] = live ? bf16_to_f32(*reinterpret_cast<const uint16_t*>(ss + 256 + row * 4)) : 0.f;
+    }
+  };
+  auto read_w = [&](int stg, int kblk, bool live) {
+    const uint8_t* ws = lds + stg * kStage + kXBytes + wave * 2048;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int row = nb * 32 + c32;
+      const uint32_t v = *reinterpret_cast<const uint32_t*>(ws + row * 32 + (2 * kblk + kh) * 4);
+      dw[nb] = live ? v : 0u;
+    }
+  };
+  // quarter q of the word of fragment nb: output register q (codes 2q, 2q+1)
+  uint32_t dlo[NB], dhi[NB];
+  auto dequant_q = [&](int nb, int kblk, int q) {
+    if (q == 0) {
+      dlo[nb] = dw[nb] & 0x0f0f0f0fu;
+      dhi[nb] = (dw[nb] >> 4) & 0x0f0f0f0fu;
+    }
+    uint32_t* o = reinterpret_cast<uint32_t*>(&bf[nb][kblk]);
+    float a, c;
+    if (q == 0) { a = ubyte<0>(dlo[nb]); c = ubyte<0>(dhi[nb]); }
+    if (q == 1) { a = ubyte<1>(dlo[nb]); c = ubyte<1>(dhi[nb]); }
+    if (q == 2) { a = ubyte<2>(dlo[nb]); c = ubyte<2>(dhi[nb]); }
+    if (q == 3) { a = ubyte<3>(dlo[nb]); c = ubyte<3>(dhi[nb]); }
+    o[q] = pk_bf16(fmaf(dsf[nb], a, dbf[nb]), fmaf(dsf[nb], c, dbf[nb]));
+  };
+  auto dequant_all = [&](int kblk) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dequant_q(nb, kblk, q);
+  };
+
+  f32x16_t acc[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // prologue: steps 0 and 1 in flight; step 0 complete, k blocks 0-2 of
+  // step 0 dequantized (k block 3 follows in step 0's k block 0).
+  issue(0, 0);
+  issue(min(1, G - 1), 1);
+  vm_wait_step();
+  __syncthreads();
+  read_sb(0, true);
+#pragma unroll
+  for (int kblk = 0; kblk < 3; ++kblk) {
+    read_w(0, kblk, true);
+    dequant_all(kblk);
+  }
+
+  // One K step = 32 sub-steps (k block kblk = st / 8, row block mb = st % 8),
+  // each: the A fragment of the next sub-step is read ahead, the 2 MFMAs
+  // of (mb, kblk) issue, then a small piece of other work:
+  //   st 0-11   one load each of step g + 2 (stage read in step g - 1)
+  //   st 0      read the words of k block 3 of step g
+  //   st 0-7    dequantize them, a quarter word per sub-step
+  //   st 7      wait for this lane's loads of step g + 1
+  //   st 8      read its scales and biases
+  //   st 8j     (j = 1, 2, 3) read the words of k block j - 1 of step g + 1
+  //   st 8j..   dequantize them (their fragments were last used in k block
+  //             j - 1 of step g)
+  //   end       barrier: X(g + 1) of every wave complete
+  // Past the last step the fragments are zero and the loads repeat the last
+  // step's addresses.
+  int stg = 0;
+  for (int g = 0; g < G; ++g) {
+    const int stg1 = stg == kStages - 1 ? 0 : stg + 1;
+    const int stg2 = stg1 == kStages - 1 ? 0 : stg1 + 1;
+    const int gn = min(g + 2, G - 1);
+    const uint8_t* xb = lds + stg * kStage;
+    const bool live1 = g + 1 < G;
+    uint4 a = *reinterpret_cast<const uint4*>(xb + aoff(0, 0));
+#pragma unroll
+    for (int st = 0; st < KB * MB; ++st) {
+      const int kblk = st / MB, mb = st % MB;
+      uint4 an = a;
+      if (st + 1 < KB * MB)
+        an = *reinterpret_cast<const uint4*>(xb + aoff((st + 1) % MB, (st + 1) / MB));
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32(a, bf[nb][kblk], acc[mb][nb]);
+#ifndef GEMM_EXP_NO_DMA
+      if (st < kDmaPerStep) issue1(gn, stg2, st);
+#endif
+      if (st == 0) read_w(stg, 3, true);
+#ifndef GEMM_EXP_NO_WAIT
+      // step g + 1's loads complete: only the 8 loads of step g + 2 issued
+      // at st 0-7 may still be in flight
+      if (st == 7) vm_wait(std::integral_constant<int, 8>{});
+#endif
+      if (st == 8) read_sb(stg1, live1);  // after the last use of step g's (st 7)
+      if (st % 8 == 0 && st > 0) read_w(stg1, kblk - 1, live1);
+#ifndef GEMM_EXP_NO_DEQ
+      {
+        const int j = st % 8;  // quarter j % 4 of fragment j / 4
+        dequant_q(j / 4, st < 8 ? 3 : kblk - 1, j % 4);
+      }
+#endif
+      __builtin_amdgcn_sched_barrier(0);
+      a = an;
+    }
+#ifndef GEMM_EXP_NO_BAR
+    __syncthreads();
+#endif
+    stg = stg1;
+  }
+  // C layout: lane holds column c32, rows 8 (i / 4) + 4 kh + i % 4.
+  YT* yb = y + (int64_t)(m0 + 4 * kh) * N + n0 + wave * WN + c32;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        Elem<YT>::store(yb, (int64_t)(mb * 32 + 8 * (i / 4) + i % 4) * N + nb * 32, acc[mb][nb][i]);
+}
+
+}  // namespace
+
+int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const uint32_t* w, const uint16_t* s,
+                               const uint16_t* b, int N, void* y, int y_dtype, void* stream) {
+  STRATA_REQUIRE(K % TK == 0 && K >= TK, "q4 GEMM: K must be a positive multiple of 64");
+  STRATA_REQUIRE(M % TM == 0 && N % TN == 0 && M > 0 && N > 0,
+                 "q4 GEMM (256-tile kernel): M and N must be positive multiples of 256");
+  STRATA_REQUIRE((uint64_t)M * K * 2 < (1ull << 32) && (uint64_t)N * K / 2 < (1ull << 32),
+                 "q4 GEMM (256-tile kernel): operands must be under 4 GiB");
+  dim3 grid((M / TM) * (N / TN));
+  constexpr size_t lds_bytes = (size_t)kStages * kStage;
+  if (y_dtype == STRATA_BF16) {
+    static bool attr = false;
+    if (!attr) {
+      STRATA_HIP_CHECK(hipFuncSetAttribute((const void*)q4_gemm_mfma_kernel<bf16_t>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes));
+      attr = true;
+    }
+    hipLaunchKernelGGL(q4_gemm_mfma_kernel<bf16_t>, grid, dim3(NTHR), lds_bytes, as_stream(stream),
+                       (const uint16_t*)x, M, K, w, s, b, N, (bf16_t*)y);
+  } else {
+    static bool attr = false;
+    if (!attr) {
+      STRATA_HIP_CHECK(hipFuncSetAttribute((const void*)q4_gemm_mfma_kernel<float>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes));
+      attr = true;
+    }
+    hipLaunchKernelGGL(q4_gemm_mfma_kernel<float>, grid, dim3(NTHR), lds_bytes, as_stream(stream),
+                       (const uint16_t*)x, M, K, w, s, b, N, (float*)y);
+  }
+  STRATA_HIP_CHECK(hipGetLastError());
+  return STRATA_OK;
+}
