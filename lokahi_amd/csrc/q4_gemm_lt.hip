@@ -196,8 +196,11 @@ int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t*
     // Full 256-row tiles on the 256 x 256 kernel, remaining rows (and any N
     // that is not a multiple of 256) on the 128 x 128 kernel.
     const int Mf = M / 256 * 256;
-    if (Mf >= kMfmaMinRows && N % 256 == 0) {
-      int rc = strata_q4_gemm_mfma_launch(x, Mf, K, w, s, b, N, y, y_dtype, stream);
+    if (Mf >= kMfmaMinRows && N % 256 == 0 && aligned16(w)) {
+      void* scr = nullptr;
+      int rc = strata_ctx_scratch(ctx, strata_q4_gemm_mfma_scratch(N, K), &scr, stream);
+      if (rc) return rc;
+      rc = strata_q4_gemm_mfma_launch(x, Mf, K, w, s, b, N, y, y_dtype, scr, stream);
       if (rc || Mf == M) return rc;
       const size_t ye = y_dtype == STRATA_BF16 ? 2 : 4;
       return strata_q4_gemm_launch(static_cast<const uint16_t*>(x) + (size_t)Mf * K, M - Mf, K,

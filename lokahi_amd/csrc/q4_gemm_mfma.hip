@@ -108,37 +108,36 @@ __device__ __forceinline__ v4i32_t rsrc(const void* p, uint32_t bytes) {
 }
 
 // Direct global -> LDS loads (buffer_load ... lds): lane l of the wave writes
-// its 16 bytes at LDS byte address lds + 16 l (2-byte loads: zero-extended
-// to 4 bytes at lds + 4 l).  Issued as inline
+// its 16 (4) bytes at LDS byte address lds + 16 l (4 l).  Issued as inline
 // assembly: the compiler does not track them, so it inserts no waits for
 // them; the kernel waits with explicit s_waitcnt vmcnt.
 __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, v4i32_t r, uint32_t soff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
 }
-__device__ __forceinline__ void dma2(uint32_t lds, uint32_t voff, v4i32_t r, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_ushort %1, %2, %3 offen lds"
+__device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, v4i32_t r, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
                :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
 }
 
 // LDS stage layout (bytes): X tile 256 x 128 (swizzled 16-byte chunks), then
-// per wave its 64 weight rows x 32 bytes, then per wave 64 scales and 64
-// biases (a 2-byte load lands zero-extended in 4 bytes of LDS).  Three
-// stages: the loads of step g + 2 are issued at the top of step g.
+// per wave its 64 weight rows x 32 bytes, then per wave 64 (s | b << 16)
+// words.  Three stages: the loads of step g + 2 are issued at the top of
+// step g.
 constexpr int kXBytes = TM * TK * 2;             // 32 KB
 constexpr int kWBytes = 4 * 64 * 32;             // 8 KB
-constexpr int kSBBytes = 4 * 64 * 4 * 2;         // 2 KB
+constexpr int kSBBytes = 4 * 64 * 4;             // 1 KB
 constexpr int kStage = kXBytes + kWBytes + kSBBytes;
 constexpr int kStages = 3;
-constexpr int kDmaPerStep = XCH + 2 + 1 + 1;     // per lane: X chunks, W halves, s, b
+constexpr int kDmaPerStep = XCH + 2 + 1;         // per lane: X chunks, W halves, (s, b)
 
 // Full tiles only: M % 256 == 0, N % 256 == 0, K % 64 == 0, and every
 // operand under 4 GiB (the launcher checks).
 template <typename YT>
 __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
-                         const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
-                         const uint16_t* __restrict__ bi, int N, YT* __restrict__ y) {
+                         const uint32_t* __restrict__ wt, const uint32_t* __restrict__ sbt,
+                         int N, YT* __restrict__ y) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int mt = M / TM, nt = N / TN;
   int tmi, tni;
@@ -148,24 +147,24 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = K / TK;
   const uint32_t kb = (uint32_t)K * 2;   // bytes per X row
-  const uint32_t wb = (uint32_t)K / 2;   // bytes per weight row
-  const uint32_t gb = (uint32_t)G * 2;   // bytes per scale row
+  const uint32_t wgb = (uint32_t)N * 32;  // bytes per group of the re-laid-out codes
+  const uint32_t sgb = (uint32_t)N * 4;   // bytes per group of (s, b) words
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(
       (__attribute__((address_space(3))) uint8_t*)lds);
 
   const v4i32_t rx = rsrc(x, (uint32_t)((size_t)M * kb));
-  const v4i32_t rw = rsrc(w, (uint32_t)((size_t)N * wb));
-  const v4i32_t rs = rsrc(sc, (uint32_t)((size_t)N * gb));
-  const v4i32_t rb = rsrc(bi, (uint32_t)((size_t)N * gb));
+  const v4i32_t rw = rsrc(wt, (uint32_t)((size_t)G * wgb));
+  const v4i32_t rs = rsrc(sbt, (uint32_t)((size_t)G * sgb));
 
   // X DMA instruction i of wave w fills 16-byte slots S = (8w + i) * 64 + lane
   // of the stage: row r = S / 8, slot p = lane % 8 holds chunk
   // c = p ^ ((r >> 1) & 7) = (lane & 7) ^ (4 (i & 1) + (lane >> 4)).
   const uint32_t xl0 = (lane >> 3) * kb + (((lane & 7) ^ (lane >> 4)) << 4);
   const uint32_t xl1 = (lane >> 3) * kb + (((lane & 7) ^ (4 + (lane >> 4))) << 4);
-  // W DMA j of this wave: 16-byte chunk q = 64 j + lane = row q/2, half q%2.
-  const uint32_t wl = (lane >> 1) * wb + (lane & 1) * 16;
-  const uint32_t sl = lane * gb;
+  // W DMA j of this wave: 16-byte chunk q = 64 j + lane = row q/2, half q%2
+  // of the group-major codes (rows of one group are 32 bytes apart).
+  const uint32_t wl = lane * 16;
+  const uint32_t sl = lane * 4;
   // DMA piece p (0 .. kDmaPerStep - 1) of step g into stage stg: X chunks
   // 0-7, the two weight halves, the scales, the biases.
   auto issue1 = [&](int g, int stg, int p) {
@@ -176,11 +175,9 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
     } else if (p < XCH + 2) {
       const int j = p - XCH;
       dma16(base + kXBytes + wave * 2048 + j * 1024, wl, rw,
-            (uint32_t)(n0 + wave * WN + j * 32) * wb + g * 32);
+            g * wgb + (uint32_t)(n0 + wave * WN + j * 32) * 32);
     } else {
-      const int h = p - XCH - 2;  // 0: scales, 1: biases
-      dma2(base + kXBytes + kWBytes + wave * 512 + h * 256, sl, h ? rb : rs,
-           (uint32_t)(n0 + wave * WN) * gb + g * 2);
+      dma4(base + kXBytes + kWBytes + wave * 256, sl, rs, g * sgb + (uint32_t)(n0 + wave * WN) * 4);
     }
   };
   auto issue = [&](int g, int stg) {
@@ -212,12 +209,12 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   uint32_t dw[NB];
   float dsf[NB], dbf[NB];
   auto read_sb = [&](int stg, bool live) {
-    const uint8_t* ss = lds + stg * kStage + kXBytes + kWBytes + wave * 512;
+    const uint8_t* ss = lds + stg * kStage + kXBytes + kWBytes + wave * 256;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      const int row = nb * 32 + c32;
-      dsf[nb] = live ? bf16_to_f32(*reinterpret_cast<const uint16_t*>(ss + row * 4)) : 0.f;
-      dbf[nb] = live ? bf16_to_f32(*reinterpret_cast<const uint16_t*>(ss + 256 + row * 4)) : 0.f;
+      const uint32_t v = *reinterpret_cast<const uint32_t*>(ss + (nb * 32 + c32) * 4);
+      dsf[nb] = live ? __uint_as_float(v << 16) : 0.f;
+      dbf[nb] = live ? __uint_as_float(v & 0xffff0000u) : 0.f;
     }
   };
   auto read_w = [&](int stg, int kblk, bool live) {
@@ -259,30 +256,28 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // prologue: steps 0 and 1 in flight; step 0 complete, k blocks 0-2 of
-  // step 0 dequantized (k block 3 follows in step 0's k block 0).
+  // prologue: steps 0 and 1 in flight; step 0 complete and its k block 0
+  // dequantized (k blocks 1-3 follow during step 0).
   issue(0, 0);
   issue(min(1, G - 1), 1);
   vm_wait_step();
   __syncthreads();
   read_sb(0, true);
-#pragma unroll
-  for (int kblk = 0; kblk < 3; ++kblk) {
-    read_w(0, kblk, true);
-    dequant_all(kblk);
-  }
+  read_w(0, 0, true);
+  dequant_all(0);
 
   // One K step = 32 sub-steps (k block kblk = st / 8, row block mb = st % 8),
   // each: the A fragment of the next sub-step is read ahead, the 2 MFMAs
-  // of (mb, kblk) issue, then a small piece of other work:
+  // of (mb, kblk) issue, then a small piece of other work.  Fragments are
+  // dequantized one k block ahead of their use, a quarter word per
+  // sub-step: during k block j the fragments of k block j + 1 (of step g,
+  // or of step g + 1 for j = 3), whose registers were last read in k block
+  // j + 1 of the previous step.
   //   st 0-11   one load each of step g + 2 (stage read in step g - 1)
-  //   st 0      read the words of k block 3 of step g
-  //   st 0-7    dequantize them, a quarter word per sub-step
-  //   st 7      wait for this lane's loads of step g + 1
-  //   st 8      read its scales and biases
-  //   st 8j     (j = 1, 2, 3) read the words of k block j - 1 of step g + 1
-  //   st 8j..   dequantize them (their fragments were last used in k block
-  //             j - 1 of step g)
+  //   st 8j     (j < 3) read the words of k block j + 1 of step g
+  //   st 23     wait for this lane's loads of step g + 1 (the 12 loads of
+  //             step g + 2 may remain in flight)
+  //   st 24     read step g + 1's scales, biases and k block 0 words
   //   end       barrier: X(g + 1) of every wave complete
   // Past the last step the fragments are zero and the loads repeat the last
   // step's addresses.
@@ -305,18 +300,18 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 #ifndef GEMM_EXP_NO_DMA
       if (st < kDmaPerStep) issue1(gn, stg2, st);
 #endif
-      if (st == 0) read_w(stg, 3, true);
+      if (st % 8 == 0 && kblk < 3) read_w(stg, kblk + 1, true);
 #ifndef GEMM_EXP_NO_WAIT
-      // step g + 1's loads complete: only the 8 loads of step g + 2 issued
-      // at st 0-7 may still be in flight
-      if (st == 7) vm_wait(std::integral_constant<int, 8>{});
+      if (st == 23) vm_wait_step();
 #endif
-      if (st == 8) read_sb(stg1, live1);  // after the last use of step g's (st 7)
-      if (st % 8 == 0 && st > 0) read_w(stg1, kblk - 1, live1);
+      if (st == 24) {
+        read_sb(stg1, live1);  // step g's last dequant was at st 23
+        read_w(stg1, 0, live1);
+      }
 #ifndef GEMM_EXP_NO_DEQ
       {
         const int j = st % 8;  // quarter j % 4 of fragment j / 4
-        dequant_q(j / 4, st < 8 ? 3 : kblk - 1, j % 4);
+        dequant_q(j / 4, (kblk + 1) % KB, j % 4);
       }
 #endif
       __builtin_amdgcn_sched_barrier(0);
@@ -338,15 +333,46 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
         Elem<YT>::store(yb, (int64_t)(mb * 32 + 8 * (i / 4) + i % 4) * N + nb * 32, acc[mb][nb][i]);
 }
 
+// Re-layout of one q4 weight for the kernel above (a pass over the weight,
+// ~1% of the GEMM at 8192 rows): codes group-major, wt[g][n][8 words], so a
+// K step's rows are contiguous; scale and bias of (n, g) packed in one word,
+// sbt[g][n] = s | b << 16.
+__global__ __launch_bounds__(256) void q4_gemm_relayout_kernel(
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
+    int N, int G, uint4* __restrict__ wt, uint32_t* __restrict__ sbt) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;  // (n, g), g fastest
+  if (i >= (int64_t)N * G) return;
+  const int n = (int)(i / G), g = (int)(i - (int64_t)n * G);
+  const uint4 lo = w[i * 2], hi = w[i * 2 + 1];
+  wt[((int64_t)g * N + n) * 2] = lo;
+  wt[((int64_t)g * N + n) * 2 + 1] = hi;
+  sbt[(int64_t)g * N + n] = (uint32_t)s[i] | ((uint32_t)b[i] << 16);
+}
+
 }  // namespace
 
+size_t strata_q4_gemm_mfma_scratch(int N, int K) {
+  return (size_t)N * K / 2 + (size_t)N * (K / TK) * 4;
+}
+
 int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const uint32_t* w, const uint16_t* s,
-                               const uint16_t* b, int N, void* y, int y_dtype, void* stream) {
+                               const uint16_t* b, int N, void* y, int y_dtype, void* scratch,
+                               void* stream) {
   STRATA_REQUIRE(K % TK == 0 && K >= TK, "q4 GEMM: K must be a positive multiple of 64");
   STRATA_REQUIRE(M % TM == 0 && N % TN == 0 && M > 0 && N > 0,
                  "q4 GEMM (256-tile kernel): M and N must be positive multiples of 256");
   STRATA_REQUIRE((uint64_t)M * K * 2 < (1ull << 32) && (uint64_t)N * K / 2 < (1ull << 32),
                  "q4 GEMM (256-tile kernel): operands must be under 4 GiB");
+  STRATA_REQUIRE(scratch && ((reinterpret_cast<uintptr_t>(scratch) | reinterpret_cast<uintptr_t>(w)) & 15) == 0,
+                 "q4 GEMM: unaligned buffers");
+  const int G = K / TK;
+  uint32_t* wt = static_cast<uint32_t*>(scratch);
+  uint32_t* sbt = wt + (size_t)N * K / 8;
+  const int64_t items = (int64_t)N * G;
+  hipLaunchKernelGGL(q4_gemm_relayout_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), reinterpret_cast<const uint4*>(w), s, b, N, G,
+                     reinterpret_cast<uint4*>(wt), sbt);
+  STRATA_HIP_CHECK(hipGetLastError());
   dim3 grid((M / TM) * (N / TN));
   constexpr size_t lds_bytes = (size_t)kStages * kStage;
   if (y_dtype == STRATA_BF16) {
@@ -357,7 +383,7 @@ int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const uint32_t* w, c
       attr = true;
     }
     hipLaunchKernelGGL(q4_gemm_mfma_kernel<bf16_t>, grid, dim3(NTHR), lds_bytes, as_stream(stream),
-                       (const uint16_t*)x, M, K, w, s, b, N, (bf16_t*)y);
+                       (const uint16_t*)x, M, K, wt, sbt, N, (bf16_t*)y);
   } else {
     static bool attr = false;
     if (!attr) {
@@ -366,7 +392,7 @@ int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const uint32_t* w, c
       attr = true;
     }
     hipLaunchKernelGGL(q4_gemm_mfma_kernel<float>, grid, dim3(NTHR), lds_bytes, as_stream(stream),
-                       (const uint16_t*)x, M, K, w, s, b, N, (float*)y);
+                       (const uint16_t*)x, M, K, wt, sbt, N, (float*)y);
   }
   STRATA_HIP_CHECK(hipGetLastError());
   return STRATA_OK;

@@ -46,8 +46,12 @@ int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t*
 void strata_gemm_lt_destroy(strata_ctx* ctx);
 // 256 x 256-tile fused-dequant MFMA GEMM (M >= kMfmaMinRows on the default path).
 constexpr int kMfmaMinRows = 256;
+// scratch: strata_q4_gemm_mfma_scratch(N, K) bytes, 16-byte aligned (the
+// weight's per-call re-layout).
+size_t strata_q4_gemm_mfma_scratch(int N, int K);
 int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const uint32_t* w, const uint16_t* s,
-                               const uint16_t* b, int N, void* y, int y_dtype, void* stream);
+                               const uint16_t* b, int N, void* y, int y_dtype, void* scratch,
+                               void* stream);
 // bf16 [N, K] = s*q + b (fp32, one RNE rounding) of a q4 triple; K % 64 == 0,
 // w and out 16-byte aligned.
 int strata_q4_dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, int64_t N,
