@@ -35,13 +35,11 @@
 
 namespace {
 
-constexpr int TM = 256, TN = 256, TK = 64;
+constexpr int TN = 256, TK = 64;
 constexpr int NTHR = 256;
 constexpr int WN = 64;              // columns per wave
-constexpr int MB = TM / 32;         // 32-row MFMA blocks per wave
 constexpr int NB = WN / 32;         // 32-column MFMA blocks per wave
 constexpr int KB = TK / 16;         // 16-deep MFMA k blocks per K step
-constexpr int XCH = TM * 8 / NTHR;  // X chunks (16 B) staged per thread per K step
 constexpr int kGroupM = 4;          // M tiles per group of the tile order
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer descriptor, gfx9 data format
 
@@ -124,20 +122,32 @@ __device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, v4i32_t r, uin
 // per wave its 64 weight rows x 32 bytes, then per wave 64 (s | b << 16)
 // words.  Three stages: the loads of step g + 2 are issued at the top of
 // step g.
-constexpr int kXBytes = TM * TK * 2;             // 32 KB
 constexpr int kWBytes = 4 * 64 * 32;             // 8 KB
 constexpr int kSBBytes = 4 * 64 * 4;             // 1 KB
-constexpr int kStage = kXBytes + kWBytes + kSBBytes;
 constexpr int kStages = 3;
-constexpr int kDmaPerStep = XCH + 2 + 1;         // per lane: X chunks, W halves, (s, b)
 
 // Full tiles only: M % 256 == 0, N % 256 == 0, K % 64 == 0, and every
 // operand under 4 GiB (the launcher checks).
-template <typename YT>
-__global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// Per-M-tile constants: TM = 256 (one workgroup per CU) or 128 (two per
+// CU, for problems with few 256-row tiles).
+template <int TM>
+struct Tile {
+  static constexpr int MB = TM / 32;                    // 32-row MFMA blocks per wave
+  static constexpr int XCH = TM * 8 / NTHR;             // X chunks (16 B) per thread per step
+  static constexpr int kXBytes = TM * TK * 2;
+  static constexpr int kStage = kXBytes + kWBytes + kSBBytes;
+  static constexpr int kDmaPerStep = XCH + 2 + 1;       // per lane: X chunks, W halves, (s, b)
+  static constexpr size_t kLds = (size_t)kStages * kStage;
+};
+
+template <int TM, typename YT>
+__global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(TM == 256 ? 1 : 2, TM == 256 ? 1 : 2)))
 void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
                          const uint32_t* __restrict__ wt, const uint32_t* __restrict__ sbt,
                          int N, YT* __restrict__ y) {
+  constexpr int MB = Tile<TM>::MB, XCH = Tile<TM>::XCH, kXBytes = Tile<TM>::kXBytes;
+  constexpr int kStage = Tile<TM>::kStage, kDmaPerStep = Tile<TM>::kDmaPerStep;
+  constexpr int QPS = 8 / MB;  // dequant quarters per sub-step
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int mt = M / TM, nt = N / TN;
   int tmi, tni;
@@ -273,11 +283,12 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   // sub-step: during k block j the fragments of k block j + 1 (of step g,
   // or of step g + 1 for j = 3), whose registers were last read in k block
   // j + 1 of the previous step.
-  //   st 0-11   one load each of step g + 2 (stage read in step g - 1)
-  //   st 8j     (j < 3) read the words of k block j + 1 of step g
-  //   st 23     wait for this lane's loads of step g + 1 (the 12 loads of
-  //             step g + 2 may remain in flight)
-  //   st 24     read step g + 1's scales, biases and k block 0 words
+  //   st < kDmaPerStep  one load each of step g + 2 (stage read in step g - 1)
+  //   first sub-step of k block j < 3: read the words of k block j + 1
+  //   last sub-step of k block 2: wait for this lane's loads of step g + 1
+  //             (the loads of step g + 2 may remain in flight)
+  //   first sub-step of k block 3: read step g + 1's scales, biases and
+  //             k block 0 words
   //   end       barrier: X(g + 1) of every wave complete
   // Past the last step the fragments are zero and the loads repeat the last
   // step's addresses.
@@ -300,17 +311,18 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 #ifndef GEMM_EXP_NO_DMA
       if (st < kDmaPerStep) issue1(gn, stg2, st);
 #endif
-      if (st % 8 == 0 && kblk < 3) read_w(stg, kblk + 1, true);
+      if (mb == 0 && kblk < 3) read_w(stg, kblk + 1, true);
 #ifndef GEMM_EXP_NO_WAIT
-      if (st == 23) vm_wait_step();
+      if (st == 3 * MB - 1) vm_wait_step();
 #endif
-      if (st == 24) {
-        read_sb(stg1, live1);  // step g's last dequant was at st 23
+      if (st == 3 * MB) {
+        read_sb(stg1, live1);  // step g's last dequant was one sub-step earlier
         read_w(stg1, 0, live1);
       }
 #ifndef GEMM_EXP_NO_DEQ
-      {
-        const int j = st % 8;  // quarter j % 4 of fragment j / 4
+#pragma unroll
+      for (int t = 0; t < QPS; ++t) {
+        const int j = mb * QPS + t;  // quarter j % 4 of fragment j / 4
         dequant_q(j / 4, (kblk + 1) % KB, j % 4);
       }
 #endif
@@ -359,7 +371,7 @@ int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const uint32_t* w, c
                                const uint16_t* b, int N, void* y, int y_dtype, void* scratch,
                                void* stream) {
   STRATA_REQUIRE(K % TK == 0 && K >= TK, "q4 GEMM: K must be a positive multiple of 64");
-  STRATA_REQUIRE(M % TM == 0 && N % TN == 0 && M > 0 && N > 0,
+  STRATA_REQUIRE(M % 256 == 0 && N % TN == 0 && M > 0 && N > 0,
                  "q4 GEMM (256-tile kernel): M and N must be positive multiples of 256");
   STRATA_REQUIRE((uint64_t)M * K * 2 < (1ull << 32) && (uint64_t)N * K / 2 < (1ull << 32),
                  "q4 GEMM (256-tile kernel): operands must be under 4 GiB");
@@ -373,27 +385,30 @@ int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const uint32_t* w, c
                      as_stream(stream), reinterpret_cast<const uint4*>(w), s, b, N, G,
                      reinterpret_cast<uint4*>(wt), sbt);
   STRATA_HIP_CHECK(hipGetLastError());
-  dim3 grid((M / TM) * (N / TN));
-  constexpr size_t lds_bytes = (size_t)kStages * kStage;
-  if (y_dtype == STRATA_BF16) {
-    static bool attr = false;
-    if (!attr) {
-      STRATA_HIP_CHECK(hipFuncSetAttribute((const void*)q4_gemm_mfma_kernel<bf16_t>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes));
-      attr = true;
-    }
-    hipLaunchKernelGGL(q4_gemm_mfma_kernel<bf16_t>, grid, dim3(NTHR), lds_bytes, as_stream(stream),
-                       (const uint16_t*)x, M, K, wt, sbt, N, (bf16_t*)y);
-  } else {
-    static bool attr = false;
-    if (!attr) {
-      STRATA_HIP_CHECK(hipFuncSetAttribute((const void*)q4_gemm_mfma_kernel<float>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes));
-      attr = true;
-    }
-    hipLaunchKernelGGL(q4_gemm_mfma_kernel<float>, grid, dim3(NTHR), lds_bytes, as_stream(stream),
-                       (const uint16_t*)x, M, K, wt, sbt, N, (float*)y);
+  // 256-row tiles unless that leaves the GPU under two workgroups per CU.
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const bool big = (int64_t)(M / 256) * (N / TN) >= 2 * cus;
+#define STRATA_GEMM_GO(TMV, YT)                                                                   \
+  {                                                                                               \
+    static bool attr = false;                                                                     \
+    if (!attr) {                                                                                  \
+      STRATA_HIP_CHECK(hipFuncSetAttribute((const void*)q4_gemm_mfma_kernel<TMV, YT>,             \
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,            \
+                                           Tile<TMV>::kLds));                                     \
+      attr = true;                                                                                \
+    }                                                                                             \
+    hipLaunchKernelGGL((q4_gemm_mfma_kernel<TMV, YT>), dim3((M / TMV) * (N / TN)), dim3(NTHR),    \
+                       Tile<TMV>::kLds, as_stream(stream), (const uint16_t*)x, M, K, wt, sbt, N,  \
+                       (YT*)y);                                                                   \
   }
+  if (y_dtype == STRATA_BF16) {
+    if (big) STRATA_GEMM_GO(256, bf16_t) else STRATA_GEMM_GO(128, bf16_t)
+  } else {
+    if (big) STRATA_GEMM_GO(256, float) else STRATA_GEMM_GO(128, float)
+  }
+#undef STRATA_GEMM_GO
   STRATA_HIP_CHECK(hipGetLastError());
   return STRATA_OK;
 }
