@@ -218,22 +218,21 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   uint4 bf[NB][KB];
   uint32_t dw[NB];
   float dsf[NB], dbf[NB];
-  auto read_sb = [&](int stg, bool live) {
+  auto read_sb = [&](int stg) {
     const uint8_t* ss = lds + stg * kStage + kXBytes + kWBytes + wave * 256;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const uint32_t v = *reinterpret_cast<const uint32_t*>(ss + (nb * 32 + c32) * 4);
-      dsf[nb] = live ? __uint_as_float(v << 16) : 0.f;
-      dbf[nb] = live ? __uint_as_float(v & 0xffff0000u) : 0.f;
+      dsf[nb] = __uint_as_float(v << 16);
+      dbf[nb] = __uint_as_float(v & 0xffff0000u);
     }
   };
-  auto read_w = [&](int stg, int kblk, bool live) {
+  auto read_w = [&](int stg, int kblk) {
     const uint8_t* ws = lds + stg * kStage + kXBytes + wave * 2048;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const int row = nb * 32 + c32;
-      const uint32_t v = *reinterpret_cast<const uint32_t*>(ws + row * 32 + (2 * kblk + kh) * 4);
-      dw[nb] = live ? v : 0u;
+      dw[nb] = *reinterpret_cast<const uint32_t*>(ws + row * 32 + (2 * kblk + kh) * 4);
     }
   };
   // quarter q of the word of fragment nb: output register q (codes 2q, 2q+1)
@@ -272,8 +271,8 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   issue(min(1, G - 1), 1);
   vm_wait_step();
   __syncthreads();
-  read_sb(0, true);
-  read_w(0, 0, true);
+  read_sb(0);
+  read_w(0, 0);
   dequant_all(0);
 
   // One K step = 32 sub-steps (k block kblk = st / 8, row block mb = st % 8),
@@ -290,15 +289,14 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   //   first sub-step of k block 3: read step g + 1's scales, biases and
   //             k block 0 words
   //   end       barrier: X(g + 1) of every wave complete
-  // Past the last step the fragments are zero and the loads repeat the last
-  // step's addresses.
+  // In the last step the loads repeat the last step's addresses and the
+  // fragments dequantized for the step after it are never used.
   int stg = 0;
   for (int g = 0; g < G; ++g) {
     const int stg1 = stg == kStages - 1 ? 0 : stg + 1;
     const int stg2 = stg1 == kStages - 1 ? 0 : stg1 + 1;
     const int gn = min(g + 2, G - 1);
     const uint8_t* xb = lds + stg * kStage;
-    const bool live1 = g + 1 < G;
     uint4 a = *reinterpret_cast<const uint4*>(xb + aoff(0, 0));
 #pragma unroll
     for (int st = 0; st < KB * MB; ++st) {
@@ -311,13 +309,13 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 #ifndef GEMM_EXP_NO_DMA
       if (st < kDmaPerStep) issue1(gn, stg2, st);
 #endif
-      if (mb == 0 && kblk < 3) read_w(stg, kblk + 1, true);
+      if (mb == 0 && kblk < 3) read_w(stg, kblk + 1);
 #ifndef GEMM_EXP_NO_WAIT
       if (st == 3 * MB - 1) vm_wait_step();
 #endif
       if (st == 3 * MB) {
-        read_sb(stg1, live1);  // step g's last dequant was one sub-step earlier
-        read_w(stg1, 0, live1);
+        read_sb(stg1);  // step g's last dequant was one sub-step earlier
+        read_w(stg1, 0);
       }
 #ifndef GEMM_EXP_NO_DEQ
 #pragma unroll
