@@ -63,9 +63,9 @@ def q4_bytes(n, k, m=1):
     return n * k // 2 + 2 * 2 * n * (k // 64) + 2 * k * m + 2 * n * m
 
 
-def graph_time_us(fn, iters, warm=2):
-    """Average duration of `fn` captured `iters` times into one HIP graph,
-    timed with events on the capture stream."""
+def graph_time_us(fn, iters, warm=2, reps=5):
+    """Duration of `fn` captured `iters` times into one HIP graph, timed with
+    events around each of `reps` replays; the median replay over `iters`."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -81,13 +81,27 @@ def graph_time_us(fn, iters, warm=2):
     g.replay()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(st)
-    g.replay()
-    b.record(st)
-    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        g.replay()
+        b.record(st)
+        torch.cuda.synchronize()
+        times.append(1e3 * a.elapsed_time(b) / iters)
     del g
-    return 1e3 * a.elapsed_time(b) / iters
+    times.sort()
+    return times[len(times) // 2]
+
+
+def rep_stats(times):
+    """min/median/p95/mean of a list of seconds, in milliseconds (the
+    warmup-then-timed-repetitions protocol of linear_projection_bench.mm:83-110)."""
+    t = sorted(times)
+    p95 = t[min(len(t) - 1, int(round(0.95 * (len(t) - 1))))]
+    return {"reps": len(t), "min_ms": round(1e3 * t[0], 3),
+            "median_ms": round(1e3 * t[len(t) // 2], 3), "p95_ms": round(1e3 * p95, 3),
+            "mean_ms": round(1e3 * sum(t) / len(t), 3)}
 
 
 def gemv_sets():
@@ -158,7 +172,7 @@ def profile_gemv(iters):
 def profile_prefill(iters=3):
     """Config 5's kernels alone (for rocprofv3 passes): the causal bf16
     attention at 8192 tokens and the 8B gate projection at M = 8192 (weight
-    dequantize + library GEMM), each ``iters`` times."""
+    re-layout + fused-dequant MFMA GEMM), each ``iters`` times."""
     import torch
     from lokahi_amd import ops
     dev = torch.device("cuda", 0)
@@ -335,10 +349,39 @@ def config1():
             "decode_us": round(graph_time_us(dec, 20), 2)}
 
 
+def _np_q4_linear(x, w, s, b):
+    """NumPy lane: dequantize the q4 matrix to float32 on every call, then
+    one BLAS matvec (q4 affine format: nibble j of word i is k = 8i + j)."""
+    import numpy as np
+    n, kw = w.shape
+    shifts = np.arange(0, 32, 4, dtype=np.uint32)
+    codes = ((w[:, :, None] >> shifts) & 0xF).astype(np.float32).reshape(n, -1, 64)
+    sf = (s.astype(np.uint32) << 16).view(np.float32)
+    bf = (b.astype(np.uint32) << 16).view(np.float32)
+    wd = (codes * sf[:, :, None] + bf[:, :, None]).reshape(n, kw * 8)
+    return wd @ x
+
+
+def _np_decode_attn(q, kc, vc):
+    """NumPy lane: one query per head against the whole cache (GQA groups)."""
+    import numpy as np
+    hq, d = q.shape
+    hkv = kc.shape[0]
+    k = (kc.astype(np.uint32) << 16).view(np.float32)
+    v = (vc.astype(np.uint32) << 16).view(np.float32)
+    qg = q.reshape(hkv, hq // hkv, d)
+    sc = np.einsum("hgd,hld->hgl", qg, k) / np.sqrt(d)
+    sc = np.exp(sc - sc.max(-1, keepdims=True))
+    sc /= sc.sum(-1, keepdims=True)
+    return np.einsum("hgl,hld->hgd", sc, v).reshape(hq, d)
+
+
 def cpu_baseline(prompt):
     """CPU restatement timed on a bounded sample: one 8B layer's seven q4
     linears, decode attention at the prompt length for one layer, and 1/8 of
-    the bf16 lm_head; scaled to one token (x32 layers, x8 lm_head)."""
+    the bf16 lm_head; scaled to one token (x32 layers, x8 lm_head).  Two
+    lanes: the C restatement (OpenMP) and NumPy (dequantize + BLAS matmul per
+    call); warmup, then timed repetitions reported as min/median/p95/mean."""
     import numpy as np
     lib_path = ROOT / "oracle" / "libstrata_oracle.so"
     lib = C.CDLL(str(lib_path))
@@ -364,7 +407,7 @@ def cpu_baseline(prompt):
     lx = np.full(4096, 0x3f80, np.uint16)
     ly = np.zeros(V8, np.float32)
 
-    def one():
+    def one_c():
         t0 = time.perf_counter()
         for n, k, w, s, b, x, y in mats:
             lib.oracle_q4_gemv_bf16(x.ctypes.data_as(P), C.c_int64(k), w.ctypes.data_as(P),
@@ -379,18 +422,40 @@ def cpu_baseline(prompt):
         t3 = time.perf_counter()
         return (t1 - t0) * 32 + (t2 - t1) * 32 + (t3 - t2) * 8
 
-    one()  # warm
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < 10.0 and len(times) < 50):
-        times.append(one())
-    times.sort()
-    per_token = times[len(times) // 2]
-    cores = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count()
-    return {"value": round(1.0 / per_token, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": (f"C restatement (OpenMP), median of {len(times)} reps of: one 8B layer's "
-                       f"7 q4 GEMVs + decode attention at L={prompt} (x32 layers) + 1/8 of the "
-                       f"bf16 lm_head (x8)")}
+    xf = {k: np.ones(k, np.float32) for k in (4096, 14336)}
+
+    def one_np():
+        t0 = time.perf_counter()
+        for n, k, w, s, b, x, y in mats:
+            _np_q4_linear(xf[k], w, s, b)
+        t1 = time.perf_counter()
+        _np_decode_attn(q[0], kc[0], vc[0])
+        t2 = time.perf_counter()
+        ((lw.astype(np.uint32) << 16).view(np.float32)) @ xf[4096]
+        t3 = time.perf_counter()
+        return (t1 - t0) * 32 + (t2 - t1) * 32 + (t3 - t2) * 8
+
+    def lane(fn, budget_s, max_reps):
+        fn()  # warm
+        times, t_start = [], time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_start < budget_s
+                                 and len(times) < max_reps):
+            times.append(fn())
+        return times
+
+    tc = lane(one_c, 10.0, 50)
+    tn = lane(one_np, 10.0, 20)
+    med_c = sorted(tc)[len(tc) // 2]
+    med_n = sorted(tn)[len(tn) // 2]
+    omp = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count()
+    sc, sn = rep_stats(tc), rep_stats(tn)
+    sc["tok_s"], sn["tok_s"] = round(1.0 / med_c, 3), round(1.0 / med_n, 3)
+    sn["cores"] = os.cpu_count()
+    return {"value": round(1.0 / med_c, 3), "unit": "tok/s", "cores": omp, "kind": "port",
+            "sample": ("C restatement (OpenMP) per token from one 8B layer's 7 q4 GEMVs + decode "
+                       f"attention at L={prompt} (x32 layers) + 1/8 of the bf16 lm_head (x8); "
+                       "value from the median repetition"),
+            "lanes": {"c_openmp_per_token": sc, "numpy_dequant_matmul_per_token": sn}}
 
 
 def main():

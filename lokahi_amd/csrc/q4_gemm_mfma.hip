@@ -212,11 +212,14 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   };
 
   // B fragment (nb, kblk) = 8 codes of row nb*32 + c32, word 2 kblk + kh of
-  // the group.  bf[nb][kblk]: frag (nb, k) of step g is rewritten for step
-  // g + 1 in the k block after its last use (k block 3 of step g + 1 during
-  // k block 0 of step g + 1).
+  // the group, found as word kblk of the row's 16-byte half kh (the re-layout
+  // stores each row as its even words, then its odd words, the two halves
+  // swapped on rows with bit 2 set so that the 8 lanes of one LDS read cycle
+  // cover all banks).  bf[nb][kblk]: frag (nb, k) of step g is rewritten for
+  // step g + 1 in the k block after its last use (k block 3 of step g + 1
+  // during k block 0 of step g + 1).
   uint4 bf[NB][KB];
-  uint32_t dw[NB];
+  uint4 dw[NB];
   float dsf[NB], dbf[NB];
   auto read_sb = [&](int stg) {
     const uint8_t* ss = lds + stg * kStage + kXBytes + kWBytes + wave * 256;
@@ -227,20 +230,20 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
       dbf[nb] = __uint_as_float(v & 0xffff0000u);
     }
   };
-  auto read_w = [&](int stg, int kblk) {
+  auto read_w = [&](int stg) {
     const uint8_t* ws = lds + stg * kStage + kXBytes + wave * 2048;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int row = nb * 32 + c32;
-      dw[nb] = *reinterpret_cast<const uint32_t*>(ws + row * 32 + (2 * kblk + kh) * 4);
-    }
+    for (int nb = 0; nb < NB; ++nb)
+      dw[nb] = *reinterpret_cast<const uint4*>(ws + (nb * 32 + c32) * 32 +
+                                               ((kh ^ ((c32 >> 2) & 1)) << 4));
   };
   // quarter q of the word of fragment nb: output register q (codes 2q, 2q+1)
   uint32_t dlo[NB], dhi[NB];
   auto dequant_q = [&](int nb, int kblk, int q) {
     if (q == 0) {
-      dlo[nb] = dw[nb] & 0x0f0f0f0fu;
-      dhi[nb] = (dw[nb] >> 4) & 0x0f0f0f0fu;
+      const uint32_t v = kblk == 0 ? dw[nb].x : kblk == 1 ? dw[nb].y : kblk == 2 ? dw[nb].z : dw[nb].w;
+      dlo[nb] = v & 0x0f0f0f0fu;
+      dhi[nb] = (v >> 4) & 0x0f0f0f0fu;
     }
     uint32_t* o = reinterpret_cast<uint32_t*>(&bf[nb][kblk]);
     float a, c;
@@ -272,7 +275,7 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   vm_wait_step();
   __syncthreads();
   read_sb(0);
-  read_w(0, 0);
+  read_w(0);
   dequant_all(0);
 
   // One K step = 32 sub-steps (k block kblk = st / 8, row block mb = st % 8),
@@ -283,11 +286,10 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   // or of step g + 1 for j = 3), whose registers were last read in k block
   // j + 1 of the previous step.
   //   st < kDmaPerStep  one load each of step g + 2 (stage read in step g - 1)
-  //   first sub-step of k block j < 3: read the words of k block j + 1
   //   last sub-step of k block 2: wait for this lane's loads of step g + 1
   //             (the loads of step g + 2 may remain in flight)
   //   first sub-step of k block 3: read step g + 1's scales, biases and
-  //             k block 0 words
+  //             code words
   //   end       barrier: X(g + 1) of every wave complete
   // In the last step the loads repeat the last step's addresses and the
   // fragments dequantized for the step after it are never used.
@@ -309,13 +311,12 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 #ifndef GEMM_EXP_NO_DMA
       if (st < kDmaPerStep) issue1(gn, stg2, st);
 #endif
-      if (mb == 0 && kblk < 3) read_w(stg, kblk + 1);
 #ifndef GEMM_EXP_NO_WAIT
       if (st == 3 * MB - 1) vm_wait_step();
 #endif
       if (st == 3 * MB) {
         read_sb(stg1);  // step g's last dequant was one sub-step earlier
-        read_w(stg1, 0);
+        read_w(stg1);
       }
 #ifndef GEMM_EXP_NO_DEQ
 #pragma unroll
@@ -345,8 +346,9 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 
 // Re-layout of one q4 weight for the kernel above (a pass over the weight,
 // ~1% of the GEMM at 8192 rows): codes group-major, wt[g][n][8 words], so a
-// K step's rows are contiguous; scale and bias of (n, g) packed in one word,
-// sbt[g][n] = s | b << 16.
+// K step's rows are contiguous, each row's words in the order 0 2 4 6 | 1 3
+// 5 7 (halves swapped when bit 2 of n is set); scale and bias of (n, g)
+// packed in one word, sbt[g][n] = s | b << 16.
 __global__ __launch_bounds__(256) void q4_gemm_relayout_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
     int N, int G, uint4* __restrict__ wt, uint32_t* __restrict__ sbt) {
@@ -354,8 +356,10 @@ __global__ __launch_bounds__(256) void q4_gemm_relayout_kernel(
   if (i >= (int64_t)N * G) return;
   const int n = (int)(i / G), g = (int)(i - (int64_t)n * G);
   const uint4 lo = w[i * 2], hi = w[i * 2 + 1];
-  wt[((int64_t)g * N + n) * 2] = lo;
-  wt[((int64_t)g * N + n) * 2 + 1] = hi;
+  const uint4 ev = make_uint4(lo.x, lo.z, hi.x, hi.z), od = make_uint4(lo.y, lo.w, hi.y, hi.w);
+  const int sw = (n >> 2) & 1;
+  wt[((int64_t)g * N + n) * 2 + sw] = ev;
+  wt[((int64_t)g * N + n) * 2 + (sw ^ 1)] = od;
   sbt[(int64_t)g * N + n] = (uint32_t)s[i] | ((uint32_t)b[i] << 16);
 }
 
