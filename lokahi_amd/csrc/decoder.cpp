@@ -367,23 +367,24 @@ int strata_decoder_generate(strata_decoder* d, const int32_t* prompt, int B, int
     RC(strata_embed_launch(d->embed, c.vocab_size, c.hidden_size, prompt, (int64_t)B * L, d->h, s));
     RC(forward_layers(d, B, L, pos0, s));
     appended = pos0 + L;
-    RC(strata_argmax_launch(d->logits, B, c.vocab_size, temperature, d->ids, d->amax, s));
-    // counters {step, position, key count}: the advance below records token 0
+    // counters {step, position, key count}: the tail below records token 0
     // and leaves {1, pos0+L, pos0+L+1}, i.e. the next step processes the token
     // at position pos0+L against pos0+L+1 keys.
     const int init[4] = {0, pos0 + L - 1, pos0 + L, 0};
     STRATA_HIP_CHECK(hipMemcpyAsync(d->counters, init, sizeof(init), hipMemcpyHostToDevice, s));
-    RC(strata_decode_advance_launch(d->ids, B, d->tokens, d->kv->Lmax, d->counters,
-                                    d->rope_table, d->kv->Lmax, c.head_dim / 2, d->rope_cur, s));
+    // Each step ends with the greedy token, its embedding in h (the next
+    // step's input) and the advanced counters.
+    auto tail = [&](hipStream_t st) -> int {
+      return strata_decode_tail_launch(d->logits, B, c.vocab_size, temperature, d->amax, d->ids,
+                                       d->tokens, d->kv->Lmax, d->counters, d->rope_table,
+                                       d->kv->Lmax, c.head_dim / 2, d->rope_cur, d->embed,
+                                       c.hidden_size, d->h, st);
+    };
+    RC(tail(s));
 
     auto decode_step = [&](hipStream_t st, int key_cap) -> int {
-      RC(strata_embed_launch(d->embed, c.vocab_size, c.hidden_size, d->ids, B, d->h, st));
       RC(forward_layers(d, B, 1, -1, st, key_cap));
-      RC(strata_argmax_launch(d->logits, B, c.vocab_size, temperature, d->ids, d->amax, st));
-      RC(strata_decode_advance_launch(d->ids, B, d->tokens, d->kv->Lmax, d->counters,
-                                      d->rope_table, d->kv->Lmax, c.head_dim / 2, d->rope_cur,
-                                      st));
-      return STRATA_OK;
+      return tail(st);
     };
     const bool reuse = d->graph_batch == B && d->graph_temp == temperature;
     if (max_new > 1 && !reuse) {

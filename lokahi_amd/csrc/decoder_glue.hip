@@ -336,6 +336,76 @@ int strata_quantize_launch(const void* src, int dtype, int64_t N, int64_t K, int
 }
 
 namespace {
+// End of a decode step in one workgroup: the greedy token of each batch row
+// from the argmax partials, recorded in ids and out[row, step]; the row's
+// embedding gathered into h for the next step (llama_mlx.py:724-738); then
+// the counters advance and the RoPE row of the new position is staged, as
+// decode_advance_kernel does.
+__global__ __launch_bounds__(256) void decode_tail_kernel(
+    const float* __restrict__ pv, const int* __restrict__ pi, int nb, int B,
+    int32_t* __restrict__ ids, int32_t* __restrict__ out, int out_stride,
+    int* __restrict__ counters, const float2* __restrict__ rope_table, int lmax, int half,
+    float2* __restrict__ rope_cur, const uint16_t* __restrict__ table, int64_t H, int vec,
+    uint16_t* __restrict__ h) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  __shared__ int sid;
+  const int step = counters[0];
+  const int pos = counters[1] + 1;
+  for (int b = 0; b < B; ++b) {
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < nb; i += 256) argmax_pick(best, bi, pv[b * nb + i], pi[b * nb + i]);
+    argmax_block(best, bi, sv, si);
+    if (threadIdx.x == 0) {
+      const int id = bi == 0x7fffffff ? 0 : bi;
+      ids[b] = id;
+      out[(int64_t)b * out_stride + step] = id;
+      sid = id;
+    }
+    __syncthreads();
+    const int64_t id = sid;
+    if (vec) {
+      const uint4* src = reinterpret_cast<const uint4*>(table + id * H);
+      uint4* dst = reinterpret_cast<uint4*>(h + (int64_t)b * H);
+      for (int64_t i = threadIdx.x; i < H / 8; i += 256) dst[i] = src[i];
+    } else {
+      for (int64_t i = threadIdx.x; i < H; i += 256) h[(int64_t)b * H + i] = table[id * H + i];
+    }
+    __syncthreads();  // sv, si, sid are reused by the next row
+  }
+  if (rope_cur && pos >= 0 && pos < lmax)
+    for (int t = threadIdx.x; t < half; t += 256) rope_cur[t] = rope_table[(int64_t)pos * half + t];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    counters[0] = step + 1;
+    counters[1] += 1;
+    counters[2] += 1;
+  }
+}
+}  // namespace
+
+int strata_decode_tail_launch(const float* logits, int B, int64_t V, float temperature,
+                              void* partial, int32_t* ids, int32_t* out_tokens, int out_stride,
+                              int* counters, const float2* rope_table, int lmax, int half,
+                              float2* rope_cur, const uint16_t* table, int64_t H, void* h,
+                              void* stream) {
+  const int nb = kArgmaxBlocks;
+  const int slice = static_cast<int>((V + nb - 1) / nb);
+  float* pv = reinterpret_cast<float*>(partial);
+  int* pi = reinterpret_cast<int*>(pv + (int64_t)B * nb);
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(nb, B), dim3(256), 0, s, logits, V, temperature,
+                     slice, pv, pi);
+  const int vec = H % 8 == 0 && ((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(h)) & 15) == 0;
+  hipLaunchKernelGGL(decode_tail_kernel, dim3(1), dim3(256), 0, s, pv, pi, nb, B, ids, out_tokens,
+                     out_stride, counters, rope_table, lmax, half, rope_cur, table, H, vec,
+                     (uint16_t*)h);
+  STRATA_HIP_CHECK(hipGetLastError());
+  return STRATA_OK;
+}
+
+namespace {
 // End of a graph-replayed decode step: record the token chosen for each batch
 // row, advance the device counters {step, position, key count}, and stage
 // the RoPE (cos, sin) row of the new position for the next step's q/k/v

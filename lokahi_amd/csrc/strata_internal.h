@@ -88,6 +88,14 @@ int strata_quantize_launch(const void* src, int dtype, int64_t N, int64_t K, int
 int strata_rope_table_launch(float2* table, int lmax, int D, float theta, void* stream);
 // Records the step's tokens, advances {step, position, key count} and, when
 // rope_cur is given, stages rope_table's row of the new position into it.
+// Greedy argmax of B logit rows (two kernels: partials, then one workgroup
+// that also records the tokens, gathers their embeddings into h and
+// advances the counters like strata_decode_advance_launch).
+int strata_decode_tail_launch(const float* logits, int B, int64_t V, float temperature,
+                              void* partial, int32_t* ids, int32_t* out_tokens, int out_stride,
+                              int* counters, const float2* rope_table, int lmax, int half,
+                              float2* rope_cur, const uint16_t* table, int64_t H, void* h,
+                              void* stream);
 int strata_decode_advance_launch(const int32_t* ids, int B, int32_t* out_tokens, int out_stride,
                                  int* counters, const float2* rope_table, int lmax, int half,
                                  float2* rope_cur, void* stream);
