@@ -483,6 +483,10 @@ void attn_prefill_mfma(
   kfull = min(kfull, __shfl_xor(kfull, 2, 64));
   kfull = min(kfull, __shfl_xor(kfull, 4, 64));
   kfull = min(kfull, __shfl_xor(kfull, 8, 64));
+  // keys any row of this wave needs (rows past Lq need none)
+  int wave_need = kneed;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) wave_need = max(wave_need, __shfl_xor(wave_need, off, 64));
 
   if (threadIdx.x == 0) s_kmax = 0;
   __syncthreads();
@@ -640,18 +644,12 @@ void attn_prefill_mfma(
     const T* vs = vs_buf[cur];
     const bool more = kb0 + KT < kmax;
     if (more) fetch(kb0 + KT);
-    // Query blocks of this wave that see any key of the tile (causal: the
-    // wave's later blocks may, its earlier ones may not, near the diagonal).
-    bool live[QB];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      int need = qp[qb] + 1;
-      need = max(need, __shfl_xor(need, 1, 64));
-      need = max(need, __shfl_xor(need, 2, 64));
-      need = max(need, __shfl_xor(need, 4, 64));
-      need = max(need, __shfl_xor(need, 8, 64));
-      live[qb] = kb0 < need;
-    }
+    // Whether any query row of this wave sees a key of the tile (causal:
+    // waves below the diagonal skip the tile's math; a block of a live wave
+    // that sees no key is masked to p = 0 and adds nothing).  Wave-uniform,
+    // so the skip is one scalar branch, not a mask around each MFMA.
+    const bool wave_live = __builtin_amdgcn_readfirstlane((int)(kb0 < wave_need)) != 0;
+    if (wave_live) {
 
     // MFMA sections run at raised wave priority, so the other wave of the
     // SIMD fills the matrix core's gaps with its softmax.
@@ -668,7 +666,7 @@ void attn_prefill_mfma(
           const uint4 a = *reinterpret_cast<const uint4*>(&ks[(16 * j + col) * (D + KPAD) + s * 32 + grp * 8]);
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
-            if (live[qb]) st[qb][j] = mfma_bf16(__builtin_bit_cast(bf16x8_t, a), qbf[qb][s], st[qb][j]);
+            st[qb][j] = mfma_bf16(__builtin_bit_cast(bf16x8_t, a), qbf[qb][s], st[qb][j]);
         }
       } else {
 #pragma unroll
@@ -676,7 +674,7 @@ void attn_prefill_mfma(
           const float a = Elem<T>::load(ks, (16 * j + col) * (D + KPAD) + s * 4 + grp);
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
-            if (live[qb]) st[qb][j] = mfma_f32(a, qf[qb][s], st[qb][j]);
+            st[qb][j] = mfma_f32(a, qf[qb][s], st[qb][j]);
         }
       }
     }
@@ -690,7 +688,6 @@ void attn_prefill_mfma(
     const bool full = kb0 + KT <= kfull;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      if (!live[qb]) continue;
       if (!full) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -765,7 +762,7 @@ void attn_prefill_mfma(
           const bf16x8_t a = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
-            if (live[qb]) acc[qb][dt] = mfma_bf16(a, pb[qb], acc[qb][dt]);
+            acc[qb][dt] = mfma_bf16(a, pb[qb], acc[qb][dt]);
         }
       }
     } else {
@@ -779,11 +776,12 @@ void attn_prefill_mfma(
             const float a = Elem<T>::load(vs, key * (D + VPAD) + dt * 16 + col);
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb)
-              if (live[qb]) acc[qb][dt] = mfma_f32(a, st[qb][j][i], acc[qb][dt]);
+              acc[qb][dt] = mfma_f32(a, st[qb][j][i], acc[qb][dt]);
           }
         }
     }
     if constexpr (kBF16) __builtin_amdgcn_s_setprio(0);
+    }  // wave_live
     if constexpr (NBUF == 2) {
       if (more) stage(cur ^ 1);  // the other buffer: last read before the previous barrier
       __syncthreads();
@@ -811,6 +809,275 @@ void attn_prefill_mfma(
 #pragma unroll
         for (int i = 0; i < 4; ++i) Elem<T>::store(orow, dt * 16 + 4 * grp + i, acc[qb][dt][i] * inv);
     }
+  }
+}
+
+// ------------------------------------------------- bf16 prefill, 32x32 tiles
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ f32x16_t mfma32_bf16(const bf16x8_t& a, const bf16x8_t& b,
+                                                f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// bf16 prefill on 32x32x16 MFMA tiles.  Same grid and workgroup geometry as
+// attn_prefill_mfma<bf16, D, 2> (128 query rows per workgroup, 64-key tiles
+// double-buffered in LDS, V staged transposed), but each wave owns one block
+// of 32 query rows: S^T = K Q^T and O^T += V^T P^T run as 32x32x16 MFMAs,
+// whose 32-cycle issue leaves room for the softmax of the other wave on the
+// SIMD, and the P^T operand is the S^T accumulator itself (no shuffles).
+// MFMA 32x32x16 layouts (wave64): A (32 x 16): lane l holds row l%32, k
+// 8(l/32) .. +8; B (16 x 32): lane l holds column l%32, the same k; C (32 x
+// 32): lane l holds column l%32, rows 8(i/4) + 4(l/32) + i%4 for i < 16.
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void attn_prefill_mfma32(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int B, int Hq, int Hkv,
+    int Lq, int Lk, int causal, float scale, float eps, int out_tm, bf16_t* __restrict__ out) {
+  constexpr int KT = 64;    // keys per tile
+  constexpr int KPAD = 8;   // K rows: D + 8 elements
+  constexpr int VPAD = 4;   // transposed V rows: KT + 4 elements (136 B)
+  constexpr int K_ELEMS = KT * (D + KPAD);
+  constexpr int V_ELEMS = D * (KT + VPAD);
+  __shared__ __attribute__((aligned(16))) uint16_t ks_buf[2][K_ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t vs_buf[2][V_ELEMS];
+  __shared__ int s_kmax;
+
+  const int G = Hq / Hkv;
+  int qt, b, hkv, hq;
+  if (!prefill_item(true, blockIdx.x, (Lq + 127) / 128, B, Hkv, G, &qt, &b, &hkv, &hq))
+    return;  // grid padding
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c32 = lane & 31, h = lane >> 5;
+  const int row = qt * 128 + 32 * wave + c32;  // this lane's query row
+  const bool row_ok = row < Lq;
+  const int qp = row_ok ? (causal ? (qpos ? qpos[(int64_t)b * Lq + row] : Lk - Lq + row) : Lk - 1)
+                        : -1;
+  // Keys every row of the wave sees (tiles below need no mask) and keys any
+  // row of it needs (tiles from there on are skipped); lanes l and l + 32
+  // hold the same row.
+  int kfull = row_ok ? (causal ? qp + 1 : Lk) : 0;
+  int wave_need = qp + 1;
+#pragma unroll
+  for (int off = 1; off < 32; off <<= 1) {
+    kfull = min(kfull, __shfl_xor(kfull, off, 64));
+    wave_need = max(wave_need, __shfl_xor(wave_need, off, 64));
+  }
+  if (threadIdx.x == 0) s_kmax = 0;
+  __syncthreads();
+  if (lane == 0) atomicMax(&s_kmax, wave_need);
+  __syncthreads();
+  const int kmax = causal ? min(Lk, s_kmax) : Lk;
+
+  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(k) + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  const uint16_t* vbase = reinterpret_cast<const uint16_t*>(v) + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+
+  // Q^T fragments (the B operand of S^T): column = this lane's row, k = the
+  // head dims 16 s + 8 h .. +8.
+  constexpr int QS = D / 16;
+  bf16x8_t qf[QS];
+  {
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(q) +
+                           (((int64_t)b * Hq + hq) * Lq + (row_ok ? row : 0)) * D;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      uint4 u = make_uint4(0, 0, 0, 0);
+      if (row_ok) u = *reinterpret_cast<const uint4*>(qrow + s * 16 + 8 * h);
+      qf[s] = __builtin_bit_cast(bf16x8_t, u);
+    }
+  }
+  constexpr int DB = D / 32;  // 32-row head-dim blocks of O^T
+  f32x16_t acc[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const float sl2 = scale * kLog2e;
+
+  // Tile loads are register-prefetched one tile ahead (issued before the
+  // tile's math, written to the other LDS stage after it).
+  constexpr int CH = 8;                          // bf16 per 16-byte chunk
+  constexpr int NCH = KT * D / CH / 256;         // K chunks per thread per tile
+  static_assert(KT * D / CH % 256 == 0 && (D / CH) % 4 == 0, "tile chunks");
+  uint4 kreg[NCH];
+  constexpr int NVB = (KT / 4) * (D / 4) / 256;  // V 4x4 blocks per thread
+  static_assert((KT / 4) * (D / 4) % 256 == 0, "V blocks must divide over the block");
+  uint2 vblk[NVB][4];
+  auto tile_slot = [&](int c, int& t, int& d0) {
+    const int ln = c & 63, blk = c >> 6;
+    t = (blk & 3) * 16 + (ln & 15);
+    d0 = ((blk >> 2) * 4 + (ln >> 4)) * CH;
+  };
+  // keys past Lk read key Lk - 1 and are zeroed after the loads
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+      int t, d0;
+      tile_slot(threadIdx.x + 256 * u, t, d0);
+      kreg[u] = *reinterpret_cast<const uint4*>(kbase + (int64_t)min(kb + t, Lk - 1) * D + d0);
+    }
+#pragma unroll
+    for (int u = 0; u < NVB; ++u) {
+      const int blk = threadIdx.x + 256 * u;
+      const int dg = blk % (D / 4), kg = blk / (D / 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        vblk[u][r] = *reinterpret_cast<const uint2*>(vbase + (int64_t)min(kb + 4 * kg + r, Lk - 1) * D + 4 * dg);
+    }
+    if (kb + KT > Lk) {
+#pragma unroll
+      for (int u = 0; u < NCH; ++u) {
+        int t, d0;
+        tile_slot(threadIdx.x + 256 * u, t, d0);
+        if (kb + t >= Lk) kreg[u] = make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < NVB; ++u) {
+        const int kg = (threadIdx.x + 256 * u) / (D / 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (kb + 4 * kg + r >= Lk) vblk[u][r] = make_uint2(0, 0);
+      }
+    }
+  };
+  // 4-key column block c4 of row d of the transposed V tile, XOR-swizzled
+  // by (d >> 5) & 3 against the staging stores' bank conflicts.
+  auto vt_at = [&](int d, int c4) { return d * (KT + VPAD) + 4 * (c4 ^ ((d >> 5) & 3)); };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+      int t, d0;
+      tile_slot(threadIdx.x + 256 * u, t, d0);
+      *reinterpret_cast<uint4*>(&ks_buf[buf][t * (D + KPAD) + d0]) = kreg[u];
+    }
+    uint16_t* vt = vs_buf[buf];
+#pragma unroll
+    for (int u = 0; u < NVB; ++u) {
+      const int blk = threadIdx.x + 256 * u;
+      const int dg = blk % (D / 4), kg = blk / (D / 4);
+      const uint2* r = vblk[u];
+      const uint32_t lo = 0x05040100u, hi = 0x07060302u;
+      const uint2 o[4] = {
+          make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, lo), __builtin_amdgcn_perm(r[3].x, r[2].x, lo)),
+          make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, hi), __builtin_amdgcn_perm(r[3].x, r[2].x, hi)),
+          make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, lo), __builtin_amdgcn_perm(r[3].y, r[2].y, lo)),
+          make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, hi), __builtin_amdgcn_perm(r[3].y, r[2].y, hi))};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<uint2*>(&vt[vt_at(4 * dg + j, kg)]) = o[j];
+    }
+  };
+  if (kmax > 0) {
+    fetch(0);
+    stage(0);
+  }
+  __syncthreads();
+  for (int kb0 = 0, it = 0; kb0 < kmax; kb0 += KT, ++it) {
+    const int cur = it & 1;
+    const uint16_t* ks = ks_buf[cur];
+    const uint16_t* vt = vs_buf[cur];
+    const bool more = kb0 + KT < kmax;
+    if (more) fetch(kb0 + KT);
+    // Waves whose rows see no key of the tile skip its math (one scalar
+    // branch); rows of a live wave that see none are masked to p = 0.
+    if (__builtin_amdgcn_readfirstlane((int)(kb0 < wave_need))) {
+      __builtin_amdgcn_s_setprio(1);
+      // st[kb][i] = score(this lane's row, key kb0 + 32 kb + 8(i/4) + 4h + i%4)
+      f32x16_t st[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[kb][r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < QS; ++s) {
+          const uint4 a = *reinterpret_cast<const uint4*>(&ks[(32 * kb + c32) * (D + KPAD) + 16 * s + 8 * h]);
+          st[kb] = mfma32_bf16(__builtin_bit_cast(bf16x8_t, a), qf[s], st[kb]);
+        }
+      }
+      __builtin_amdgcn_s_setprio(0);
+      // online softmax in the log2 domain (raw scores kept; the scale is
+      // folded into the exponent's FMA, sl2 > 0)
+      if (kb0 + KT > kfull) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = kb0 + 32 * kb + 8 * (i / 4) + 4 * h + i % 4;
+            const bool ok = key < Lk && (!causal || key <= qp) && row_ok;
+            st[kb][i] = ok ? st[kb][i] : -INFINITY;
+          }
+      }
+      float mb = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mb = fmaxf(mb, st[kb][i]);
+      mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+      const float mn = fmaxf(m_run, mb * sl2);
+      // rows with no visible key yet keep mn = -inf (weights 0, alpha 1)
+      const bool none = mn == -INFINITY;
+      const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
+      const float nmn = none ? 0.f : -mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(st[kb][i], sl2, nmn));  // exp2(-inf) = 0
+          st[kb][i] = p;
+          ps += p;
+        }
+      l_run = fmaf(l_run, alpha, ps);
+      m_run = mn;
+      if (__any(alpha != 1.f)) {
+#pragma unroll
+        for (int i = 0; i < DB; ++i) acc[i] *= alpha;
+      }
+      __builtin_amdgcn_s_setprio(1);
+      // O^T += V^T P^T over 16-key steps: the P^T operand of step s4 (keys
+      // 16 s4 .. +16) is st[s4 / 2][8 (s4 % 2) .. +8]: lane half h holds keys
+      // 16 s4 + 4h + 0..3 and 16 s4 + 8 + 4h + 0..3, and the V^T operand of
+      // row d takes the same keys from transposed 4-key blocks 4 s4 + h and
+      // 4 s4 + 2 + h.
+#pragma unroll
+      for (int s4 = 0; s4 < KT / 16; ++s4) {
+        const int kb = s4 / 2, i0 = 8 * (s4 % 2);
+        uint4 pu;
+        pu.x = pack_bf16x2(st[kb][i0 + 0], st[kb][i0 + 1]);
+        pu.y = pack_bf16x2(st[kb][i0 + 2], st[kb][i0 + 3]);
+        pu.z = pack_bf16x2(st[kb][i0 + 4], st[kb][i0 + 5]);
+        pu.w = pack_bf16x2(st[kb][i0 + 6], st[kb][i0 + 7]);
+        const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, pu);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const int d = 32 * db + c32;
+          const uint2 lo = *reinterpret_cast<const uint2*>(vt + vt_at(d, 4 * s4 + h));
+          const uint2 hi = *reinterpret_cast<const uint2*>(vt + vt_at(d, 4 * s4 + 2 + h));
+          const bf16x8_t a = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+          acc[db] = mfma32_bf16(a, pb, acc[db]);
+        }
+      }
+      __builtin_amdgcn_s_setprio(0);
+    }
+    if (more) stage(cur ^ 1);  // the other stage: last read before the previous barrier
+    __syncthreads();
+  }
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (row_ok) {
+    const float inv = 1.f / fmaxf(l_tot, eps);
+    // out_tm: token-major [B, Lq, Hq, D] (the o_proj input); else [B, Hq, Lq, D]
+    uint16_t* orow = reinterpret_cast<uint16_t*>(out) +
+                     (out_tm ? (((int64_t)b * Lq + row) * Hq + hq) * D
+                             : (((int64_t)b * Hq + hq) * Lq + row) * D);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const uint2 o2 = make_uint2(pack_bf16x2(acc[db][4 * g4] * inv, acc[db][4 * g4 + 1] * inv),
+                                    pack_bf16x2(acc[db][4 * g4 + 2] * inv, acc[db][4 * g4 + 3] * inv));
+        *reinterpret_cast<uint2*>(orow + 32 * db + 8 * g4 + 4 * h) = o2;
+      }
   }
 }
 
@@ -984,10 +1251,27 @@ int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v,
   }
   if constexpr (sizeof(TQ) == sizeof(TK) && sizeof(TK) == sizeof(TV)) {
     if (Lq > 1 && (D == 64 || D == 128)) {
-      // bf16: two 16-row query blocks per wave (128 queries per workgroup)
+      // bf16: 128 queries per workgroup on 32x32x16 tiles
       constexpr int QB = sizeof(TQ) == 2 ? 2 : 1;
       const int nqt = (Lq + 64 * QB - 1) / (64 * QB);
       dim3 grid(prefill_grid(nqt, B, Hkv, Hq / Hkv));
+      static const bool old16 = getenv("STRATA_ATTN_PREFILL16") != nullptr;
+      if constexpr (sizeof(TQ) == 2) {
+        if (!old16) {
+          if (D == 64)
+            hipLaunchKernelGGL((attn_prefill_mfma32<64>), grid, dim3(256), 0, stream,
+                               (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, kv_bs, kv_hs,
+                               qpos, B, Hq, Hkv, Lq, Lk, causal, scale, eps, ex.out_tm,
+                               (bf16_t*)out);
+          else
+            hipLaunchKernelGGL((attn_prefill_mfma32<128>), grid, dim3(256), 0, stream,
+                               (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, kv_bs, kv_hs,
+                               qpos, B, Hq, Hkv, Lq, Lk, causal, scale, eps, ex.out_tm,
+                               (bf16_t*)out);
+          STRATA_HIP_CHECK(hipGetLastError());
+          return STRATA_OK;
+        }
+      }
       if (D == 64)
         hipLaunchKernelGGL((attn_prefill_mfma<TQ, 64, QB>), grid, dim3(256), 0, stream,
                            (const TQ*)q, (const TQ*)k, (const TQ*)v, kv_bs, kv_hs, qpos, B, Hq,
