@@ -6,19 +6,20 @@
 // accumulated online in fp32, out = wv / max(s, eps) in q's dtype.  Query
 // positions default to bottom-right alignment arange(Lk - Lq, Lk) (69-72).
 //
-// Three kernels:
+// Kernels:
 //   * attn_decode_kernel : Lq == 1.  Split-K over the key axis; each workgroup
 //     streams one key chunk of one KV head for its query heads (the whole
 //     group G = Hq/Hkv, K/V read once, or half of it when the grid would not
 //     fill the GPU), keeps per-16-lane online-softmax state in registers,
 //     merges its lanes through LDS and writes (m, s, o[D]) partials;
 //     attn_decode_merge combines the chunks.
-//   * attn_prefill_mfma : Lq > 1, D in {64, 128}, q/k/v of one dtype.
-//     Flash-style: 64-key K / V^T tiles staged in LDS, S^T = K Q^T and
-//     O^T += V^T P^T on MFMA (bf16 16x16x32, or f32 16x16x4 for fp32 inputs),
-//     so every lane owns one query row (of each of the wave's 16-row query
-//     blocks) and all softmax state is in-lane.  Key blocks past the causal
-//     limit of the workgroup's query tile are skipped.
+//   * attn_prefill_mfma32 : Lq > 1, bf16 q/k/v, D in {64, 128}.  Flash-style
+//     on 32x32x16 MFMA: 64-key K and V tiles streamed straight from global
+//     memory into LDS (two stages), S^T = K Q^T and O^T += V^T P^T, every
+//     lane owns one query row and all softmax state is in-lane; V^T
+//     operands come from row-major V through the LDS transpose read.  Key
+//     tiles past the causal limit of the workgroup's query tile are skipped.
+//   * attn_prefill_f32 : the same for fp32 inputs on 16x16x4 fp32 MFMA.
 //   * attn_generic : any other shape (e.g. tiny head dims), one wave per query.
 #include <algorithm>
 #include <cstdlib>
@@ -409,9 +410,6 @@ __device__ inline bool prefill_item(bool remap, int wg, int nqt, int B, int Hkv,
   *hq = *hkv * G + g;
   return true;
 }
-__device__ __forceinline__ f32x4_t mfma_bf16(const bf16x8_t& a, const bf16x8_t& b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
 __device__ __forceinline__ f32x4_t mfma_f32(float a, float b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -422,393 +420,176 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// 1-D grid, block 256; workgroup -> (query tile qt, b, hq) by prefill_item:
-// the G query heads of one KV head and query tile run on one XCD in
-// consecutive slots (their K/V tiles share that XCD's L2) and the longest
-// causal query tiles are dispatched first.  Wave w owns QB blocks of 16
-// query rows, qt*64*QB + 16*(QB*w + qb) + 0..15.  Every K / V^T operand read from
-// LDS feeds the QB blocks' MFMAs (QB = 2 halves the LDS traffic per flop).
-// MFMA 16x16 layouts used (wave64, gfx950):
-//   A (16 x K): lane l holds row l%16, k-slots (l/16)*KS .. +KS
-//   B (K x 16): lane l holds col l%16, k-slots (l/16)*KS .. +KS
-//   C (16x16) : lane l holds col l%16, rows (l/16)*4 + 0..3
-// with KS = 8 for bf16 16x16x32 and KS = 1 for f32 16x16x4.
-template <typename T, int D, int QB>
-// Two query blocks per wave need 2 waves per SIMD to hide the tile loads:
-// the VGPR budget is capped there (fits without spills).
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 2 ? 2 : 1)))
-void attn_prefill_mfma(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, int64_t kv_bs,
-    int64_t kv_hs, const int32_t* __restrict__ qpos, int B, int Hq, int Hkv, int Lq, int Lk,
-    int causal, float scale, float eps, int out_tm, T* __restrict__ out) {
-  constexpr bool kBF16 = sizeof(T) == 2;
-  constexpr int KT = 64;                         // keys per tile
-  constexpr int KPAD = kBF16 ? 8 : 4;            // LDS row padding (elements)
-  // bf16 V is stored transposed [D][KT + VPAD]: rows of 68 elements (136 B)
-  // keep the 8-byte reads and writes aligned.
-  constexpr int VPAD = 4;
-  // K tile: [KT][D + KPAD]; V tile: bf16 -> transposed [D][KT + VPAD], f32 -> [KT][D + VPAD]
-  constexpr int K_ELEMS = KT * (D + KPAD);
-  constexpr int V_ELEMS = kBF16 ? D * (KT + VPAD) : KT * (D + VPAD);
-  // bf16: two LDS stages (2 x 34.8 KB; gfx950 allows 160 KB per workgroup)
-  // so tile t+1 is staged while other waves still compute on tile t, one
-  // barrier per tile.  fp32 tiles are twice as large: one stage.
-  constexpr int NBUF = kBF16 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) T ks_buf[NBUF][K_ELEMS];
-  __shared__ __attribute__((aligned(16))) T vs_buf[NBUF][V_ELEMS];
+// fp32 prefill.  1-D grid, block 256; workgroup -> (query tile qt, b, hq)
+// in plain order (prefill_item without the remap); wave w owns the 16 query
+// rows qt*64 + 16w + 0..15.  S^T = K Q^T and O^T += V P^T on 16x16x4 fp32
+// MFMAs; one LDS stage of K and V tiles (64 keys, row-major, padded rows).
+// MFMA 16x16x4 layouts (wave64): A (16 x 4): lane l holds row l%16, k l/16;
+// B (4 x 16): lane l holds column l%16, k l/16; C (16 x 16): lane l holds
+// column l%16, rows 4(l/16) + 0..3.
+template <int D>
+__global__ __launch_bounds__(256) void attn_prefill_f32(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int B, int Hq, int Hkv,
+    int Lq, int Lk, int causal, float scale, float eps, int out_tm, float* __restrict__ out) {
+  constexpr int KT = 64;                 // keys per tile
+  constexpr int PAD = 4;                 // LDS row padding (elements)
+  constexpr int RS = D + PAD;            // LDS row stride
+  __shared__ __attribute__((aligned(16))) float ks[KT * RS];
+  __shared__ __attribute__((aligned(16))) float vs[KT * RS];
   __shared__ int s_kmax;
 
   const int G = Hq / Hkv;
   int qt, b, hkv, hq;
-  if (!prefill_item(QB == 2, blockIdx.x, (Lq + 64 * QB - 1) / (64 * QB), B, Hkv, G, &qt, &b,
-                    &hkv, &hq))
+  if (!prefill_item(false, blockIdx.x, (Lq + 63) / 64, B, Hkv, G, &qt, &b, &hkv, &hq))
     return;  // grid padding
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, grp = lane >> 4;
-  int row[QB], qp[QB];
-  bool row_ok[QB];
-  int kfull = Lk, kneed = 0;
+  const int row = qt * 64 + 16 * wave + col;  // this lane's query row
+  const bool row_ok = row < Lq;
+  const int qp = row_ok ? (causal ? (qpos ? qpos[(int64_t)b * Lq + row] : Lk - Lq + row) : Lk - 1)
+                        : -1;
+  // keys every row of the wave sees (no mask below) and keys any row needs
+  int kfull = row_ok ? (causal ? qp + 1 : Lk) : 0;
+  int wave_need = qp + 1;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    row[qb] = qt * 64 * QB + 16 * (QB * wave + qb) + col;  // this lane's query rows
-    row_ok[qb] = row[qb] < Lq;
-    qp[qb] = -1;
-    if (row_ok[qb])
-      qp[qb] = causal ? (qpos ? qpos[(int64_t)b * Lq + row[qb]] : Lk - Lq + row[qb]) : Lk - 1;
-    kneed = max(kneed, qp[qb] + 1);
-    // key tiles below kfull are visible to every row of this wave (no mask)
-    kfull = min(kfull, row_ok[qb] ? (causal ? qp[qb] + 1 : Lk) : 0);
+  for (int off = 1; off < 16; off <<= 1) {
+    kfull = min(kfull, __shfl_xor(kfull, off, 64));
+    wave_need = max(wave_need, __shfl_xor(wave_need, off, 64));
   }
-  kfull = min(kfull, __shfl_xor(kfull, 1, 64));
-  kfull = min(kfull, __shfl_xor(kfull, 2, 64));
-  kfull = min(kfull, __shfl_xor(kfull, 4, 64));
-  kfull = min(kfull, __shfl_xor(kfull, 8, 64));
-  // keys any row of this wave needs (rows past Lq need none)
-  int wave_need = kneed;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) wave_need = max(wave_need, __shfl_xor(wave_need, off, 64));
-
   if (threadIdx.x == 0) s_kmax = 0;
   __syncthreads();
-  if (grp == 0) atomicMax(&s_kmax, kneed);
+  if (lane == 0) atomicMax(&s_kmax, wave_need);
   __syncthreads();
   const int kmax = causal ? min(Lk, s_kmax) : Lk;
 
-  const T* kbase = k + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
-  const T* vbase = v + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
-
-  // Q fragments as the B operand of S^T = K Q^T: col = query row, k = head dim.
-  constexpr int QF = kBF16 ? D / 32 : D / 4;
-  bf16x8_t qbf[QB][kBF16 ? QF : 1];
-  float qf[QB][kBF16 ? 1 : QF];
+  const float* kbase = k + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  const float* vbase = v + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  // Q fragments as the B operand of S^T: column = query row, k = head dim 4s + grp.
+  constexpr int QF = D / 4;
+  float qf[QF];
+  {
+    const float* qrow = q + (((int64_t)b * Hq + hq) * Lq + (row_ok ? row : 0)) * D;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const T* qrow = q + (((int64_t)b * Hq + hq) * Lq + (row_ok[qb] ? row[qb] : 0)) * D;
-    if constexpr (kBF16) {
-#pragma unroll
-      for (int s = 0; s < QF; ++s) {
-        uint4 u = make_uint4(0, 0, 0, 0);
-        if (row_ok[qb]) u = *reinterpret_cast<const uint4*>(qrow + s * 32 + grp * 8);
-        qbf[qb][s] = __builtin_bit_cast(bf16x8_t, u);
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < QF; ++s) qf[qb][s] = row_ok[qb] ? Elem<T>::load(qrow, s * 4 + grp) : 0.f;
-    }
+    for (int s = 0; s < QF; ++s) qf[s] = row_ok ? qrow[4 * s + grp] : 0.f;
   }
-
   constexpr int DT = D / 16;  // output d tiles
-  f32x4_t acc[QB][DT];
-  float m_run[QB], l_run[QB];
+  f32x4_t acc[DT];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-#pragma unroll
-    for (int i = 0; i < DT; ++i) acc[qb][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    m_run[qb] = -INFINITY;
-    l_run[qb] = 0.f;
-  }
+  for (int i = 0; i < DT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = scale * kLog2e;
 
-  // K/V tiles are register-prefetched: tile t+1's global loads are issued
-  // right after tile t is written to LDS, so they are in flight during the
-  // tile's MFMAs and softmax.
-  constexpr int CH = 16 / sizeof(T);            // elements per 16-byte chunk
-  constexpr int NCH = KT * D / CH / 256;        // chunks per thread per tile
-  static_assert(KT * D / CH % 256 == 0, "tile chunks must divide over the block");
+  // Tiles: 16-byte chunks, chunk c of the tile -> (key t, element d0); keys
+  // past Lk read key Lk - 1 (finite; their scores are masked, their
+  // weights 0).  Tile t+1's loads are issued before tile t's math.
+  constexpr int NCH = KT * D / 4 / 256;  // chunks per thread per tile
+  static_assert(KT * D / 4 % 256 == 0, "tile chunks must divide over the block");
   uint4 kreg[NCH], vreg[NCH];
-  // bf16 V is fetched as 4 keys x 4 head-dim blocks (8 bytes per key) and
-  // transposed in registers (v_perm), so each block is four 8-byte LDS rows
-  // of the [D][KT + VPAD] tile instead of sixteen 2-byte stores.
-  constexpr int NVB = kBF16 ? (KT / 4) * (D / 4) / 256 : 1;  // 4x4 blocks per thread
-  static_assert(!kBF16 || (KT / 4) * (D / 4) % 256 == 0, "V blocks must divide over the block");
-  uint2 vblk[NVB][4];
-  // chunk c of the tile -> (key t, element d0): each wave covers 16 keys x 4
-  // consecutive 16-byte chunks (64-byte row segments).
-  auto tile_slot = [&](int c, int& t, int& d0) {
-    const int ln = c & 63, blk = c >> 6;
-    t = (blk & 3) * 16 + (ln & 15);
-    d0 = ((blk >> 2) * 4 + (ln >> 4)) * CH;
-  };
-  static_assert((D / CH) % 4 == 0, "tile_slot needs a multiple of 4 chunks per key");
-  // Keys past Lk read key Lk-1 (clamped, no load behind a branch) and are
-  // zeroed after the loads when the tile runs past the end.
   auto fetch = [&](int kb) {
-    const bool tail = kb + KT > Lk;
 #pragma unroll
     for (int u = 0; u < NCH; ++u) {
       const int c = threadIdx.x + 256 * u;
-      int t, d0;
-      tile_slot(c, t, d0);
+      const int t = c / (D / 4), d0 = 4 * (c % (D / 4));
       const int key = min(kb + t, Lk - 1);
       kreg[u] = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * D + d0);
-      if constexpr (!kBF16) vreg[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * D + d0);
-    }
-    if constexpr (kBF16) {
-#pragma unroll
-      for (int u = 0; u < NVB; ++u) {
-        const int blk = threadIdx.x + 256 * u;
-        const int dg = blk % (D / 4), kg = blk / (D / 4);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = min(kb + 4 * kg + r, Lk - 1);
-          vblk[u][r] = *reinterpret_cast<const uint2*>(vbase + (int64_t)key * D + 4 * dg);
-        }
-      }
-    }
-    if (tail) {
-#pragma unroll
-      for (int u = 0; u < NCH; ++u) {
-        const int c = threadIdx.x + 256 * u;
-        int t, d0;
-        tile_slot(c, t, d0);
-        if (kb + t >= Lk) {
-          kreg[u] = make_uint4(0, 0, 0, 0);
-          if constexpr (!kBF16) vreg[u] = make_uint4(0, 0, 0, 0);
-        }
-      }
-      if constexpr (kBF16) {
-#pragma unroll
-        for (int u = 0; u < NVB; ++u) {
-          const int kg = (threadIdx.x + 256 * u) / (D / 4);
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (kb + 4 * kg + r >= Lk) vblk[u][r] = make_uint2(0, 0);
-        }
-      }
+      vreg[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * D + d0);
     }
   };
-  // Element offset of 4-key column block c4 of row d in the transposed V
-  // tile.  The block index is XORed with (d >> 5) & 3: the staging stores of
-  // 32 lanes (head-dim blocks 0..31, rows 4 apart) otherwise meet every 8
-  // lanes on the same banks; a 16-row read group never crosses 32 rows, so
-  // the MFMA operand reads keep their pattern.
-  auto vt_at = [&](int d, int c4) { return d * (KT + VPAD) + 4 * (c4 ^ ((d >> 5) & 3)); };
-  // ---- stage K (row-major, padded) and V (bf16: transposed) tiles
-  auto stage = [&](int buf) {
+  auto stage = [&]() {
 #pragma unroll
     for (int u = 0; u < NCH; ++u) {
       const int c = threadIdx.x + 256 * u;
-      int t, d0;
-      tile_slot(c, t, d0);
-      *reinterpret_cast<uint4*>(&ks_buf[buf][t * (D + KPAD) + d0]) = kreg[u];
-      if constexpr (!kBF16) *reinterpret_cast<uint4*>(&vs_buf[buf][t * (D + VPAD) + d0]) = vreg[u];
-    }
-    if constexpr (kBF16) {
-      uint16_t* vt = reinterpret_cast<uint16_t*>(vs_buf[buf]);
-#pragma unroll
-      for (int u = 0; u < NVB; ++u) {
-        const int blk = threadIdx.x + 256 * u;
-        const int dg = blk % (D / 4), kg = blk / (D / 4);
-        const uint2* r = vblk[u];
-        // row j of the transposed block: (V[4kg+0..3][4dg+j]) as one uint2
-        const uint32_t lo = 0x05040100u, hi = 0x07060302u;
-        const uint2 o[4] = {
-            make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, lo), __builtin_amdgcn_perm(r[3].x, r[2].x, lo)),
-            make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, hi), __builtin_amdgcn_perm(r[3].x, r[2].x, hi)),
-            make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, lo), __builtin_amdgcn_perm(r[3].y, r[2].y, lo)),
-            make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, hi), __builtin_amdgcn_perm(r[3].y, r[2].y, hi))};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          *reinterpret_cast<uint2*>(&vt[vt_at(4 * dg + j, kg)]) = o[j];
-      }
+      const int t = c / (D / 4), d0 = 4 * (c % (D / 4));
+      *reinterpret_cast<uint4*>(&ks[t * RS + d0]) = kreg[u];
+      *reinterpret_cast<uint4*>(&vs[t * RS + d0]) = vreg[u];
     }
   };
   if (kmax > 0) {
     fetch(0);
-    stage(0);
+    stage();
   }
   __syncthreads();
-  for (int kb0 = 0, it = 0; kb0 < kmax; kb0 += KT, ++it) {
-    const int cur = NBUF == 2 ? (it & 1) : 0;
-    const T* ks = ks_buf[cur];
-    const T* vs = vs_buf[cur];
+  for (int kb0 = 0; kb0 < kmax; kb0 += KT) {
     const bool more = kb0 + KT < kmax;
     if (more) fetch(kb0 + KT);
-    // Whether any query row of this wave sees a key of the tile (causal:
-    // waves below the diagonal skip the tile's math; a block of a live wave
-    // that sees no key is masked to p = 0 and adds nothing).  Wave-uniform,
-    // so the skip is one scalar branch, not a mask around each MFMA.
-    const bool wave_live = __builtin_amdgcn_readfirstlane((int)(kb0 < wave_need)) != 0;
-    if (wave_live) {
-
-    // MFMA sections run at raised wave priority, so the other wave of the
-    // SIMD fills the matrix core's gaps with its softmax.
-    if constexpr (kBF16) __builtin_amdgcn_s_setprio(1);
-    // ---- S^T tiles: st[qb][j][i] = score(query row of block qb, key kb0 + 16j + 4*grp + i)
-    f32x4_t st[QB][4];
+    if (__builtin_amdgcn_readfirstlane((int)(kb0 < wave_need))) {
+      // st[j][i] = score(this lane's row, key kb0 + 16j + 4 grp + i)
+      f32x4_t st[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 4; ++j) {
+        st[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) st[qb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      if constexpr (kBF16) {
-#pragma unroll
-        for (int s = 0; s < QF; ++s) {
-          const uint4 a = *reinterpret_cast<const uint4*>(&ks[(16 * j + col) * (D + KPAD) + s * 32 + grp * 8]);
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-            st[qb][j] = mfma_bf16(__builtin_bit_cast(bf16x8_t, a), qbf[qb][s], st[qb][j]);
-        }
-      } else {
-#pragma unroll
-        for (int s = 0; s < QF; ++s) {
-          const float a = Elem<T>::load(ks, (16 * j + col) * (D + KPAD) + s * 4 + grp);
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-            st[qb][j] = mfma_f32(a, qf[qb][s], st[qb][j]);
-        }
+        for (int s = 0; s < QF; ++s)
+          st[j] = mfma_f32(ks[(16 * j + col) * RS + 4 * s + grp], qf[s], st[j]);
       }
-    }
-
-    if constexpr (kBF16) __builtin_amdgcn_s_setprio(0);
-    // ---- online softmax (log2 domain), all state for this lane's query rows.
-    // Raw scores are kept; the scale goes into the exponent's FMA
-    // (sl2 > 0, so max(s * sl2) = sl2 * max(s)).  Tiles every row of the
-    // wave sees in full skip the mask.  v_exp_f32 is used directly: results
-    // below 2^-126 flush to 0, far under eps.
-    const bool full = kb0 + KT <= kfull;
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      if (!full) {
+      if (kb0 + KT > kfull) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = kb0 + 16 * j + 4 * grp + i;
-            const bool ok = key < Lk && (!causal || key <= qp[qb]) && row_ok[qb];
-            st[qb][j][i] = ok ? st[qb][j][i] : -INFINITY;
+            const bool ok = key < Lk && (!causal || key <= qp) && row_ok;
+            st[j][i] = ok ? st[j][i] : -INFINITY;
           }
       }
+      // online softmax (log2 domain, raw scores kept, sl2 > 0)
       float mb = -INFINITY;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mb = fmaxf(mb, st[qb][j][i]);
+        for (int i = 0; i < 4; ++i) mb = fmaxf(mb, st[j][i]);
       mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
       mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-      const float mn = fmaxf(m_run[qb], mb * sl2);
-      float alpha, ps = 0.f;
-      const float nmn = -mn;
-      if (full) {  // every score finite: mn finite
-        alpha = __builtin_amdgcn_exp2f(m_run[qb] - mn);
+      const float mn = fmaxf(m_run, mb * sl2);
+      const bool none = mn == -INFINITY;  // no visible key yet: weights 0, alpha 1
+      const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
+      const float nmn = none ? 0.f : -mn;
+      float ps = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = __builtin_amdgcn_exp2f(fmaf(st[qb][j][i], sl2, nmn));
-            st[qb][j][i] = p;
-            ps += p;
-          }
-      } else {  // rows with no visible key yet keep mn = -inf
-        alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run[qb] - mn);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p =
-                (mn == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(fmaf(st[qb][j][i], sl2, nmn));
-            st[qb][j][i] = p;
-            ps += p;
-          }
-      }
-      l_run[qb] = fmaf(l_run[qb], alpha, ps);
-      m_run[qb] = mn;
-      if (__any(alpha != 1.f)) {  // the running max of some row moved
-#pragma unroll
-        for (int i = 0; i < DT; ++i) acc[qb][i] *= alpha;
-      }
-    }
-
-    if constexpr (kBF16) __builtin_amdgcn_s_setprio(1);
-    // ---- O^T += V^T P^T
-    if constexpr (kBF16) {
-      const uint16_t* vt = reinterpret_cast<const uint16_t*>(vs);
-#pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
-        bf16x8_t pb[QB];
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          uint4 pu;
-          pu.x = pack_bf16x2(st[qb][2 * c2][0], st[qb][2 * c2][1]);
-          pu.y = pack_bf16x2(st[qb][2 * c2][2], st[qb][2 * c2][3]);
-          pu.z = pack_bf16x2(st[qb][2 * c2 + 1][0], st[qb][2 * c2 + 1][1]);
-          pu.w = pack_bf16x2(st[qb][2 * c2 + 1][2], st[qb][2 * c2 + 1][3]);
-          pb[qb] = __builtin_bit_cast(bf16x8_t, pu);
+        for (int i = 0; i < 4; ++i) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(st[j][i], sl2, nmn));
+          st[j][i] = p;
+          ps += p;
         }
+      l_run = fmaf(l_run, alpha, ps);
+      m_run = mn;
+      if (__any(alpha != 1.f)) {
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const int d = dt * 16 + col;
-          const uint2 lo = *reinterpret_cast<const uint2*>(vt + vt_at(d, 8 * c2 + grp));
-          const uint2 hi = *reinterpret_cast<const uint2*>(vt + vt_at(d, 8 * c2 + 4 + grp));
-          const bf16x8_t a = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-            acc[qb][dt] = mfma_bf16(a, pb[qb], acc[qb][dt]);
-        }
+        for (int i = 0; i < DT; ++i) acc[i] *= alpha;
       }
-    } else {
+      // O^T += V^T P^T, one key per MFMA k-slot
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = 16 * j + 4 * grp + i;
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const float a = Elem<T>::load(vs, key * (D + VPAD) + dt * 16 + col);
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb)
-              acc[qb][dt] = mfma_f32(a, st[qb][j][i], acc[qb][dt]);
-          }
+          for (int dt = 0; dt < DT; ++dt)
+            acc[dt] = mfma_f32(vs[key * RS + dt * 16 + col], st[j][i], acc[dt]);
         }
     }
-    if constexpr (kBF16) __builtin_amdgcn_s_setprio(0);
-    }  // wave_live
-    if constexpr (NBUF == 2) {
-      if (more) stage(cur ^ 1);  // the other buffer: last read before the previous barrier
+    __syncthreads();  // every wave is done with the tile
+    if (more) {
+      stage();
       __syncthreads();
-    } else {
-      __syncthreads();  // every wave is done with the single buffer
-      if (more) {
-        stage(0);
-        __syncthreads();
-      }
     }
   }
 
+  float l_tot = l_run;
+  l_tot += __shfl_xor(l_tot, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  if (row_ok) {
+    const float inv = 1.f / fmaxf(l_tot, eps);
+    // out_tm: token-major [B, Lq, Hq, D] (the o_proj input); else [B, Hq, Lq, D]
+    float* orow = out + (out_tm ? (((int64_t)b * Lq + row) * Hq + hq) * D
+                                : (((int64_t)b * Hq + hq) * Lq + row) * D);
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    float l_tot = l_run[qb];
-    l_tot += __shfl_xor(l_tot, 16, 64);
-    l_tot += __shfl_xor(l_tot, 32, 64);
-    if (row_ok[qb]) {
-      const float inv = 1.f / fmaxf(l_tot, eps);
-      // out_tm: token-major [B, Lq, Hq, D] (the o_proj input); else [B, Hq, Lq, D]
-      T* orow = out + (out_tm ? (((int64_t)b * Lq + row[qb]) * Hq + hq) * D
-                              : (((int64_t)b * Hq + hq) * Lq + row[qb]) * D);
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) Elem<T>::store(orow, dt * 16 + 4 * grp + i, acc[qb][dt][i] * inv);
-    }
+      for (int i = 0; i < 4; ++i) orow[dt * 16 + 4 * grp + i] = acc[dt][i] * inv;
   }
 }
 
@@ -819,37 +600,48 @@ __device__ __forceinline__ f32x16_t mfma32_bf16(const bf16x8_t& a, const bf16x8_
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// bf16 prefill on 32x32x16 MFMA tiles.  Same grid and workgroup geometry as
-// attn_prefill_mfma<bf16, D, 2> (128 query rows per workgroup, 64-key tiles
-// double-buffered in LDS, V staged transposed), but each wave owns one block
-// of 32 query rows: S^T = K Q^T and O^T += V^T P^T run as 32x32x16 MFMAs,
-// whose 32-cycle issue leaves room for the softmax of the other wave on the
-// SIMD, and the P^T operand is the S^T accumulator itself (no shuffles).
+// bf16 prefill on 32x32x16 MFMA tiles.  Workgroup = 8 waves = 256 query
+// rows of one (b, query head) (grid order as prefill_item); wave w owns rows
+// qt*256 + 32w + 0..31.  S^T = K Q^T and O^T += V^T P^T run as 32x32x16
+// MFMAs whose 32-cycle issue leaves room for the other wave's softmax on the
+// SIMD; the P^T operand is the S^T accumulator itself (no shuffles).
+// K and V tiles (64 keys) are streamed by direct global -> LDS loads into a
+// ring of three stages, row-major with XOR-swizzled 16-byte chunks: the
+// loads of tile t + 2 are issued at the top of tile t, so two tiles of math
+// cover their latency, and no register holds them.  V^T operands come from
+// row-major V through the LDS transpose read (ds_read_b64_tr_b16: in each
+// 16-lane group, lane l' receives element (l' & 3) of the 4-element rows
+// addressed by lanes 4k + (l' >> 2), k < 4).
 // MFMA 32x32x16 layouts (wave64): A (32 x 16): lane l holds row l%32, k
 // 8(l/32) .. +8; B (16 x 32): lane l holds column l%32, the same k; C (32 x
 // 32): lane l holds column l%32, rows 8(i/4) + 4(l/32) + i%4 for i < 16.
-template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+template <int D, int NW, int NST>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_prefill_mfma32(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int B, int Hq, int Hkv,
     int Lq, int Lk, int causal, float scale, float eps, int out_tm, bf16_t* __restrict__ out) {
-  constexpr int KT = 64;    // keys per tile
-  constexpr int KPAD = 8;   // K rows: D + 8 elements
-  constexpr int VPAD = 4;   // transposed V rows: KT + 4 elements (136 B)
-  constexpr int K_ELEMS = KT * (D + KPAD);
-  constexpr int V_ELEMS = D * (KT + VPAD);
-  __shared__ __attribute__((aligned(16))) uint16_t ks_buf[2][K_ELEMS];
-  __shared__ __attribute__((aligned(16))) uint16_t vs_buf[2][V_ELEMS];
+  constexpr int KT = 64;              // keys per tile
+  constexpr int ROW = D * 2;          // bytes per K / V row
+  constexpr int NCHK = D / 8;         // 16-byte chunks per row
+  constexpr int TILE = KT * ROW;      // bytes of one K or V tile
+  constexpr int STAGE = 2 * TILE;     // K tile, then V tile
+  constexpr int AHEAD = NST - 1;      // tiles in flight ahead of the one computed
+  constexpr int QR = 32 * NW;         // query rows per workgroup
+  constexpr int NI = KT * NCHK / (64 * NW);  // 16-byte loads per thread per tile and operand
+  static_assert(NI >= 1 && KT * NCHK % (64 * NW) == 0, "tile loads must divide over the workgroup");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[NST * STAGE];
   __shared__ int s_kmax;
 
   const int G = Hq / Hkv;
   int qt, b, hkv, hq;
-  if (!prefill_item(true, blockIdx.x, (Lq + 127) / 128, B, Hkv, G, &qt, &b, &hkv, &hq))
+  if (!prefill_item(true, blockIdx.x, (Lq + QR - 1) / QR, B, Hkv, G, &qt, &b, &hkv, &hq))
     return;  // grid padding
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c32 = lane & 31, h = lane >> 5;
-  const int row = qt * 128 + 32 * wave + c32;  // this lane's query row
+  const int row = qt * QR + 32 * wave + c32;  // this lane's query row
   const bool row_ok = row < Lq;
   const int qp = row_ok ? (causal ? (qpos ? qpos[(int64_t)b * Lq + row] : Lk - Lq + row) : Lk - 1)
                         : -1;
@@ -869,8 +661,37 @@ void attn_prefill_mfma32(
   __syncthreads();
   const int kmax = causal ? min(Lk, s_kmax) : Lk;
 
-  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(k) + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
-  const uint16_t* vbase = reinterpret_cast<const uint16_t*>(v) + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  // Buffer descriptors of this head's K and V rows: keys at or past Lk
+  // read as zero.
+  const v4i32_t rk = rsrc(k + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs, (uint32_t)Lk * ROW);
+  const v4i32_t rv = rsrc(v + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs, (uint32_t)Lk * ROW);
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) uint8_t*)lds);
+  // Chunk swizzles.  K: the 16 lanes reading one 16-byte column of 16 rows
+  // meet 16 distinct chunk slots per 256 bytes of rows.  V: a transpose
+  // read's half-wave (4 rows, two 32-byte column pairs per row) meets 8
+  // distinct pairs per 256 bytes of rows.
+  auto fk = [](int key) { return (key / (256 / ROW)) & (NCHK - 1); };
+  auto fv = [](int key) { return (key * (NCHK / 4)) & (NCHK - 1); };
+  // Load i of this thread fills 16-byte slot (wave * NI + i) * 64 + lane of
+  // a tile: key slot / NCHK, chunk slot % NCHK holding source chunk
+  // (slot % NCHK) ^ swizzle(key).
+  uint32_t kvo[NI], vvo[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int slot = (wave * NI + i) * 64 + lane;
+    const int key = slot / NCHK, cp = slot % NCHK;
+    kvo[i] = key * ROW + 16 * (cp ^ fk(key));
+    vvo[i] = key * ROW + 16 * (cp ^ fv(key));
+  }
+  auto issue = [&](int kb, int st) {
+    const uint32_t base = lds0 + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      dma16(base + (wave * NI + i) * 1024, kvo[i], rk, (uint32_t)kb * ROW);
+      dma16(base + TILE + (wave * NI + i) * 1024, vvo[i], rv, (uint32_t)kb * ROW);
+    }
+  };
 
   // Q^T fragments (the B operand of S^T): column = this lane's row, k = the
   // head dims 16 s + 8 h .. +8.
@@ -895,105 +716,55 @@ void attn_prefill_mfma32(
   float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = scale * kLog2e;
 
-  // Tile loads are register-prefetched one tile ahead (issued before the
-  // tile's math, written to the other LDS stage after it).
-  constexpr int CH = 8;                          // bf16 per 16-byte chunk
-  constexpr int NCH = KT * D / CH / 256;         // K chunks per thread per tile
-  static_assert(KT * D / CH % 256 == 0 && (D / CH) % 4 == 0, "tile chunks");
-  uint4 kreg[NCH];
-  constexpr int NVB = (KT / 4) * (D / 4) / 256;  // V 4x4 blocks per thread
-  static_assert((KT / 4) * (D / 4) % 256 == 0, "V blocks must divide over the block");
-  uint2 vblk[NVB][4];
-  auto tile_slot = [&](int c, int& t, int& d0) {
-    const int ln = c & 63, blk = c >> 6;
-    t = (blk & 3) * 16 + (ln & 15);
-    d0 = ((blk >> 2) * 4 + (ln >> 4)) * CH;
+  // LDS byte offsets inside a stage that do not change between tiles.
+  // K operand of S^T block kb, step s: row 32 kb + c32, chunk 2s + h.
+  const int k_row_off = c32 * ROW;
+  const int k_swz = fk(c32);  // == fk(32 kb + c32)
+  // V^T operand (transpose read) of 16-key step s4, half j (keys 16 s4 + 8j
+  // + 4h + 0..3) and head-dim block db: this lane addresses key
+  // 16 s4 + 8j + 4h + (l' >> 2), head dims 32 db + 16 (g & 1) + 4 (l' & 3)
+  // .. +3, g = lane / 16, l' = lane % 16.
+  const int lp = lane & 15, g = lane >> 4;
+  const int v_key = 4 * h + (lp >> 2);      // plus 16 s4 + 8 j
+  const int v_col = 16 * (g & 1) + 4 * (lp & 3);  // plus 32 db (elements)
+
+  // Wait until at most n tiles' loads (2 NI each) of this thread are in flight.
+  auto wait_tiles = [&](int n) {
+    if (n <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if (n == 1) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * NI) : "memory");
+    else if (n == 2) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(4 * NI) : "memory");
+    else asm volatile("s_waitcnt vmcnt(%0)" :: "n"(6 * NI) : "memory");
   };
-  // keys past Lk read key Lk - 1 and are zeroed after the loads
-  auto fetch = [&](int kb) {
-#pragma unroll
-    for (int u = 0; u < NCH; ++u) {
-      int t, d0;
-      tile_slot(threadIdx.x + 256 * u, t, d0);
-      kreg[u] = *reinterpret_cast<const uint4*>(kbase + (int64_t)min(kb + t, Lk - 1) * D + d0);
-    }
-#pragma unroll
-    for (int u = 0; u < NVB; ++u) {
-      const int blk = threadIdx.x + 256 * u;
-      const int dg = blk % (D / 4), kg = blk / (D / 4);
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        vblk[u][r] = *reinterpret_cast<const uint2*>(vbase + (int64_t)min(kb + 4 * kg + r, Lk - 1) * D + 4 * dg);
-    }
-    if (kb + KT > Lk) {
-#pragma unroll
-      for (int u = 0; u < NCH; ++u) {
-        int t, d0;
-        tile_slot(threadIdx.x + 256 * u, t, d0);
-        if (kb + t >= Lk) kreg[u] = make_uint4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int u = 0; u < NVB; ++u) {
-        const int kg = (threadIdx.x + 256 * u) / (D / 4);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (kb + 4 * kg + r >= Lk) vblk[u][r] = make_uint2(0, 0);
-      }
-    }
-  };
-  // 4-key column block c4 of row d of the transposed V tile, XOR-swizzled
-  // by (d >> 5) & 3 against the staging stores' bank conflicts.
-  auto vt_at = [&](int d, int c4) { return d * (KT + VPAD) + 4 * (c4 ^ ((d >> 5) & 3)); };
-  auto stage = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < NCH; ++u) {
-      int t, d0;
-      tile_slot(threadIdx.x + 256 * u, t, d0);
-      *reinterpret_cast<uint4*>(&ks_buf[buf][t * (D + KPAD) + d0]) = kreg[u];
-    }
-    uint16_t* vt = vs_buf[buf];
-#pragma unroll
-    for (int u = 0; u < NVB; ++u) {
-      const int blk = threadIdx.x + 256 * u;
-      const int dg = blk % (D / 4), kg = blk / (D / 4);
-      const uint2* r = vblk[u];
-      const uint32_t lo = 0x05040100u, hi = 0x07060302u;
-      const uint2 o[4] = {
-          make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, lo), __builtin_amdgcn_perm(r[3].x, r[2].x, lo)),
-          make_uint2(__builtin_amdgcn_perm(r[1].x, r[0].x, hi), __builtin_amdgcn_perm(r[3].x, r[2].x, hi)),
-          make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, lo), __builtin_amdgcn_perm(r[3].y, r[2].y, lo)),
-          make_uint2(__builtin_amdgcn_perm(r[1].y, r[0].y, hi), __builtin_amdgcn_perm(r[3].y, r[2].y, hi))};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) *reinterpret_cast<uint2*>(&vt[vt_at(4 * dg + j, kg)]) = o[j];
-    }
-  };
-  if (kmax > 0) {
-    fetch(0);
-    stage(0);
-  }
+  static_assert(AHEAD <= 3, "wait_tiles covers up to three tiles in flight");
+  const int nt = (kmax + KT - 1) / KT;
+  // prologue: tiles 0 .. AHEAD - 1 in flight, tile 0 complete
+  for (int t = 0; t < AHEAD && t < nt; ++t) issue(t * KT, t);
+  wait_tiles(min(nt, AHEAD) - 1);
   __syncthreads();
-  for (int kb0 = 0, it = 0; kb0 < kmax; kb0 += KT, ++it) {
-    const int cur = it & 1;
-    const uint16_t* ks = ks_buf[cur];
-    const uint16_t* vt = vs_buf[cur];
-    const bool more = kb0 + KT < kmax;
-    if (more) fetch(kb0 + KT);
+  int st = 0;
+  for (int t = 0; t < nt; ++t) {
+    const int kb0 = t * KT;
+    if (t + AHEAD < nt) issue((t + AHEAD) * KT, (t + AHEAD) % NST);  // the stage tile t - 1 used
+    const uint8_t* ks = lds + st * STAGE;
+    const uint8_t* vs = ks + TILE;
     // Waves whose rows see no key of the tile skip its math (one scalar
     // branch); rows of a live wave that see none are masked to p = 0.
     if (__builtin_amdgcn_readfirstlane((int)(kb0 < wave_need))) {
       __builtin_amdgcn_s_setprio(1);
       // st[kb][i] = score(this lane's row, key kb0 + 32 kb + 8(i/4) + 4h + i%4)
-      f32x16_t st[2];
+      f32x16_t sc[2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) st[kb][r] = 0.f;
+        for (int r = 0; r < 16; ++r) sc[kb][r] = 0.f;
 #pragma unroll
-        for (int s = 0; s < QS; ++s) {
-          const uint4 a = *reinterpret_cast<const uint4*>(&ks[(32 * kb + c32) * (D + KPAD) + 16 * s + 8 * h]);
-          st[kb] = mfma32_bf16(__builtin_bit_cast(bf16x8_t, a), qf[s], st[kb]);
+      for (int s = 0; s < QS; ++s)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const uint4 a = *reinterpret_cast<const uint4*>(
+              ks + 32 * kb * ROW + k_row_off + 16 * ((2 * s + h) ^ k_swz));
+          sc[kb] = mfma32_bf16(__builtin_bit_cast(bf16x8_t, a), qf[s], sc[kb]);
         }
-      }
       __builtin_amdgcn_s_setprio(0);
       // online softmax in the log2 domain (raw scores kept; the scale is
       // folded into the exponent's FMA, sl2 > 0)
@@ -1004,14 +775,14 @@ void attn_prefill_mfma32(
           for (int i = 0; i < 16; ++i) {
             const int key = kb0 + 32 * kb + 8 * (i / 4) + 4 * h + i % 4;
             const bool ok = key < Lk && (!causal || key <= qp) && row_ok;
-            st[kb][i] = ok ? st[kb][i] : -INFINITY;
+            sc[kb][i] = ok ? sc[kb][i] : -INFINITY;
           }
       }
       float mb = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mb = fmaxf(mb, st[kb][i]);
+        for (int i = 0; i < 16; ++i) mb = fmaxf(mb, sc[kb][i]);
       mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
       const float mn = fmaxf(m_run, mb * sl2);
       // rows with no visible key yet keep mn = -inf (weights 0, alpha 1)
@@ -1023,8 +794,8 @@ void attn_prefill_mfma32(
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(st[kb][i], sl2, nmn));  // exp2(-inf) = 0
-          st[kb][i] = p;
+          const float p = __builtin_amdgcn_exp2f(fmaf(sc[kb][i], sl2, nmn));  // exp2(-inf) = 0
+          sc[kb][i] = p;
           ps += p;
         }
       l_run = fmaf(l_run, alpha, ps);
@@ -1035,32 +806,44 @@ void attn_prefill_mfma32(
       }
       __builtin_amdgcn_s_setprio(1);
       // O^T += V^T P^T over 16-key steps: the P^T operand of step s4 (keys
-      // 16 s4 .. +16) is st[s4 / 2][8 (s4 % 2) .. +8]: lane half h holds keys
-      // 16 s4 + 4h + 0..3 and 16 s4 + 8 + 4h + 0..3, and the V^T operand of
-      // row d takes the same keys from transposed 4-key blocks 4 s4 + h and
-      // 4 s4 + 2 + h.
+      // 16 s4 .. +16) is sc[s4 / 2][8 (s4 % 2) .. +8]: lane half h holds keys
+      // 16 s4 + 4h + 0..3 and 16 s4 + 8 + 4h + 0..3, and the V^T operand
+      // takes the same keys for its head dim.
 #pragma unroll
       for (int s4 = 0; s4 < KT / 16; ++s4) {
         const int kb = s4 / 2, i0 = 8 * (s4 % 2);
         uint4 pu;
-        pu.x = pack_bf16x2(st[kb][i0 + 0], st[kb][i0 + 1]);
-        pu.y = pack_bf16x2(st[kb][i0 + 2], st[kb][i0 + 3]);
-        pu.z = pack_bf16x2(st[kb][i0 + 4], st[kb][i0 + 5]);
-        pu.w = pack_bf16x2(st[kb][i0 + 6], st[kb][i0 + 7]);
+        pu.x = pack_bf16x2(sc[kb][i0 + 0], sc[kb][i0 + 1]);
+        pu.y = pack_bf16x2(sc[kb][i0 + 2], sc[kb][i0 + 3]);
+        pu.z = pack_bf16x2(sc[kb][i0 + 4], sc[kb][i0 + 5]);
+        pu.w = pack_bf16x2(sc[kb][i0 + 6], sc[kb][i0 + 7]);
         const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, pu);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const int d = 32 * db + c32;
-          const uint2 lo = *reinterpret_cast<const uint2*>(vt + vt_at(d, 4 * s4 + h));
-          const uint2 hi = *reinterpret_cast<const uint2*>(vt + vt_at(d, 4 * s4 + 2 + h));
-          const bf16x8_t a = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
-          acc[db] = mfma32_bf16(a, pb, acc[db]);
+          v4i16_t vv[2];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int key = 16 * s4 + 8 * j + v_key;
+            const int col = 32 * db + v_col;  // multiple of 4 elements
+            const int off = key * ROW + 16 * ((col / 8) ^ fv(key)) + 2 * (col % 8);
+            vv[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) v4i16_t*)(lds0 + (uint32_t)(vs - lds) + off));
+          }
+          uint4 au;
+          au.x = (uint16_t)vv[0][0] | ((uint32_t)(uint16_t)vv[0][1] << 16);
+          au.y = (uint16_t)vv[0][2] | ((uint32_t)(uint16_t)vv[0][3] << 16);
+          au.z = (uint16_t)vv[1][0] | ((uint32_t)(uint16_t)vv[1][1] << 16);
+          au.w = (uint16_t)vv[1][2] | ((uint32_t)(uint16_t)vv[1][3] << 16);
+          acc[db] = mfma32_bf16(__builtin_bit_cast(bf16x8_t, au), pb, acc[db]);
         }
       }
       __builtin_amdgcn_s_setprio(0);
     }
-    if (more) stage(cur ^ 1);  // the other stage: last read before the previous barrier
+    // tile t + 1 complete in this thread (later tiles' loads may remain in
+    // flight), then in every thread
+    wait_tiles(min(nt - 1, t + AHEAD) - (t + 1));
     __syncthreads();
+    st = st == NST - 1 ? 0 : st + 1;
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
@@ -1251,35 +1034,34 @@ int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v,
   }
   if constexpr (sizeof(TQ) == sizeof(TK) && sizeof(TK) == sizeof(TV)) {
     if (Lq > 1 && (D == 64 || D == 128)) {
-      // bf16: 128 queries per workgroup on 32x32x16 tiles
-      constexpr int QB = sizeof(TQ) == 2 ? 2 : 1;
-      const int nqt = (Lq + 64 * QB - 1) / (64 * QB);
-      dim3 grid(prefill_grid(nqt, B, Hkv, Hq / Hkv));
-      static const bool old16 = getenv("STRATA_ATTN_PREFILL16") != nullptr;
       if constexpr (sizeof(TQ) == 2) {
-        if (!old16) {
-          if (D == 64)
-            hipLaunchKernelGGL((attn_prefill_mfma32<64>), grid, dim3(256), 0, stream,
-                               (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, kv_bs, kv_hs,
-                               qpos, B, Hq, Hkv, Lq, Lk, causal, scale, eps, ex.out_tm,
-                               (bf16_t*)out);
-          else
-            hipLaunchKernelGGL((attn_prefill_mfma32<128>), grid, dim3(256), 0, stream,
-                               (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, kv_bs, kv_hs,
-                               qpos, B, Hq, Hkv, Lq, Lk, causal, scale, eps, ex.out_tm,
-                               (bf16_t*)out);
-          STRATA_HIP_CHECK(hipGetLastError());
-          return STRATA_OK;
-        }
+        // 4 waves (128 query rows) per workgroup, two LDS stages: two
+        // workgroups per CU, whose waves share each SIMD without sharing a
+        // barrier (8k causal: 635 us; 8 waves with 3 or 4 stages in one
+        // workgroup per CU: 685-696 us)
+        constexpr int NWV = 4, NSTV = 2;
+        const dim3 grid(prefill_grid((Lq + 32 * NWV - 1) / (32 * NWV), B, Hkv, Hq / Hkv));
+        if (D == 64)
+          hipLaunchKernelGGL((attn_prefill_mfma32<64, NWV, NSTV>), grid, dim3(64 * NWV), 0, stream,
+                             (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, kv_bs, kv_hs,
+                             qpos, B, Hq, Hkv, Lq, Lk, causal, scale, eps, ex.out_tm, (bf16_t*)out);
+        else
+          hipLaunchKernelGGL((attn_prefill_mfma32<128, NWV, NSTV>), grid, dim3(64 * NWV), 0,
+                             stream, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, kv_bs,
+                             kv_hs, qpos, B, Hq, Hkv, Lq, Lk, causal, scale, eps, ex.out_tm,
+                             (bf16_t*)out);
+      } else {
+        // fp32: 16x16x4 MFMA tiles, 64 query rows per workgroup
+        const dim3 grid(prefill_grid((Lq + 63) / 64, B, Hkv, Hq / Hkv));
+        if (D == 64)
+          hipLaunchKernelGGL((attn_prefill_f32<64>), grid, dim3(256), 0, stream,
+                             (const float*)q, (const float*)k, (const float*)v, kv_bs, kv_hs, qpos,
+                             B, Hq, Hkv, Lq, Lk, causal, scale, eps, ex.out_tm, (float*)out);
+        else
+          hipLaunchKernelGGL((attn_prefill_f32<128>), grid, dim3(256), 0, stream,
+                             (const float*)q, (const float*)k, (const float*)v, kv_bs, kv_hs, qpos,
+                             B, Hq, Hkv, Lq, Lk, causal, scale, eps, ex.out_tm, (float*)out);
       }
-      if (D == 64)
-        hipLaunchKernelGGL((attn_prefill_mfma<TQ, 64, QB>), grid, dim3(256), 0, stream,
-                           (const TQ*)q, (const TQ*)k, (const TQ*)v, kv_bs, kv_hs, qpos, B, Hq,
-                           Hkv, Lq, Lk, causal, scale, eps, ex.out_tm, (TQ*)out);
-      else
-        hipLaunchKernelGGL((attn_prefill_mfma<TQ, 128, QB>), grid, dim3(256), 0, stream,
-                           (const TQ*)q, (const TQ*)k, (const TQ*)v, kv_bs, kv_hs, qpos, B, Hq,
-                           Hkv, Lq, Lk, causal, scale, eps, ex.out_tm, (TQ*)out);
       STRATA_HIP_CHECK(hipGetLastError());
       return STRATA_OK;
     }

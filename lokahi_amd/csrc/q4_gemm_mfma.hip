@@ -41,7 +41,6 @@ constexpr int WN = 64;              // columns per wave
 constexpr int NB = WN / 32;         // 32-column MFMA blocks per wave
 constexpr int KB = TK / 16;         // 16-deep MFMA k blocks per K step
 constexpr int kGroupM = 4;          // M tiles per group of the tile order
-constexpr int kRsrcWord3 = 0x00020000;  // raw buffer descriptor, gfx9 data format
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
@@ -92,30 +91,6 @@ __device__ __forceinline__ void tile_of(int b, int mt, int nt, int* tm, int* tn)
   const int gm = min(kGroupM, mt - grp * kGroupM);
   *tm = grp * kGroupM + rem % gm;
   *tn = rem / gm;
-}
-
-typedef int v4i32_t __attribute__((ext_vector_type(4)));
-
-// Raw buffer descriptor (wave-uniform) for `bytes` bytes at p.
-__device__ __forceinline__ v4i32_t rsrc(const void* p, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(p);
-  v4i32_t r = {(int)(uint32_t)a, (int)((a >> 32) & 0xffffu), (int)bytes, kRsrcWord3};
-  r.x = __builtin_amdgcn_readfirstlane(r.x);
-  r.y = __builtin_amdgcn_readfirstlane(r.y);
-  return r;
-}
-
-// Direct global -> LDS loads (buffer_load ... lds): lane l of the wave writes
-// its 16 (4) bytes at LDS byte address lds + 16 l (4 l).  Issued as inline
-// assembly: the compiler does not track them, so it inserts no waits for
-// them; the kernel waits with explicit s_waitcnt vmcnt.
-__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, v4i32_t r, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, v4i32_t r, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
-               :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
 }
 
 // LDS stage layout (bytes): X tile 256 x 128 (swizzled 16-byte chunks), then

@@ -18,6 +18,32 @@ __device__ __forceinline__ uint4 load_nt(const uint4* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// ---------------------------------------------------------- buffer loads
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer descriptor, gfx9 data format
+typedef int v4i32_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor (wave-uniform) for `bytes` bytes at p.
+__device__ __forceinline__ v4i32_t rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  v4i32_t r = {(int)(uint32_t)a, (int)((a >> 32) & 0xffffu), (int)bytes, kRsrcWord3};
+  r.x = __builtin_amdgcn_readfirstlane(r.x);
+  r.y = __builtin_amdgcn_readfirstlane(r.y);
+  return r;
+}
+
+// Direct global -> LDS loads (buffer_load ... lds): lane l of the wave writes
+// its 16 (4) bytes at LDS byte address lds + 16 l (4 l).  Issued as inline
+// assembly: the compiler does not track them, so it inserts no waits for
+// them; the kernel waits with explicit s_waitcnt vmcnt.
+__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, v4i32_t r, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, v4i32_t r, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+
 // ---------------------------------------------------------------- bf16 <-> f32
 // bf16 values travel as uint16_t bit patterns (upper half of an IEEE f32).
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
