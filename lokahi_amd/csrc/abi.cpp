@@ -141,14 +141,8 @@ int strata_linear_q4_multi(strata_ctx* ctx, const void* x, int x_dtype, int64_t 
   }
   STRATA_REQUIRE(rows <= INT32_MAX, "too many output rows");
   if (M == 0) return STRATA_OK;
-  if (M > 8 && x_dtype == STRATA_BF16) {
-    for (int i = 0; i < count; ++i) {
-      rc = strata_q4_gemm(ctx, x, (int)M, (int)K, weights[i].w, weights[i].scales,
-                          weights[i].biases, (int)weights[i].N, weights[i].y, y_dtype, stream);
-      if (rc) return rc;
-    }
-    return STRATA_OK;
-  }
+  if (M > 8 && x_dtype == STRATA_BF16)
+    return strata_q4_gemm_multi(ctx, x, (int)M, (int)K, weights, count, y_dtype, stream);
   return strata_q4_gemv(ctx, x, x_dtype, (int)M, (int)K, weights, count, y_dtype, stream);
 }
 

@@ -158,9 +158,7 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
     qkv[2].y = d->v;
     void* kc = kv->kl(li);
     void* vc = kv->vl(li);
-    for (auto& w : qkv)
-      RC(strata_q4_gemm(d->ctx, d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
-                               stream));
+    RC(strata_q4_gemm_multi(d->ctx, d->xn, T, H, qkv, 3, STRATA_BF16, stream));
     RC(strata_rope_kv_fused_launch(d->q, d->k, d->v, STRATA_BF16, B, Hq, Hkv, L, D, kv->Lmax,
                                    pos0, nullptr, c.rope_theta, d->qr, kc, vc, STRATA_BF16,
                                    stream));
@@ -177,9 +175,7 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
     strata_q4_weight gu[2] = {Lw.gate, Lw.up};
     gu[0].y = d->gate;
     gu[1].y = d->up;
-    for (auto& w : gu)
-      RC(strata_q4_gemm(d->ctx, d->xn, T, H, w.w, w.scales, w.biases, (int)w.N, w.y, STRATA_BF16,
-                               stream));
+    RC(strata_q4_gemm_multi(d->ctx, d->xn, T, H, gu, 2, STRATA_BF16, stream));
     RC(strata_silu_mul_launch(d->gate, d->up, (int64_t)T * F, d->act, stream));
     strata_q4_weight dn = Lw.down;
     dn.y = d->delta;

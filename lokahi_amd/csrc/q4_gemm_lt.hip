@@ -184,30 +184,64 @@ void strata_gemm_lt_destroy(strata_ctx* ctx) {
   ctx->lt = nullptr;
 }
 
+int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
+                         int count, int y_dtype, void* stream) {
+  // Default: the hand-written kernels only (fused dequant, bf16 MFMA):
+  // full 256-row tiles of every linear in one launch of the 256 x 256
+  // kernel, remaining rows (and linears whose N is not a multiple of 256)
+  // on the 128 x 128 kernel.  STRATA_GEMM_LT_MIN_M > 0 opts into the
+  // dequantize + hipBLASLt path from that many rows (comparison runs only).
+  const char* e = getenv("STRATA_GEMM_LT_MIN_M");
+  const int min_rows = e ? atoi(e) : 0;
+  const size_t ye = y_dtype == STRATA_BF16 ? 2 : 4;
+  if (min_rows > 0 && M >= min_rows) {
+    for (int i = 0; i < count; ++i) {
+      const int rc = strata_q4_gemm(ctx, x, M, K, ws[i].w, ws[i].scales, ws[i].biases,
+                                    (int)ws[i].N, ws[i].y, y_dtype, stream);
+      if (rc) return rc;
+    }
+    return STRATA_OK;
+  }
+  const int Mf = M / 256 * 256;
+  strata_q4_weight big[kMaxGemmProblems];
+  int nbig = 0;
+  int64_t Nbig = 0;
+  for (int i = 0; i < count; ++i) {
+    const bool fits = Mf >= kMfmaMinRows && ws[i].N % 256 == 0 && aligned16(ws[i].w) &&
+                      nbig < kMaxGemmProblems;
+    if (fits) {
+      big[nbig++] = ws[i];
+      Nbig += ws[i].N;
+    } else {
+      const int rc = strata_q4_gemm_launch(x, M, K, ws[i].w, ws[i].scales, ws[i].biases,
+                                           (int)ws[i].N, ws[i].y, y_dtype, stream);
+      if (rc) return rc;
+    }
+  }
+  if (nbig == 0) return STRATA_OK;
+  void* scr = nullptr;
+  int rc = strata_ctx_scratch(ctx, strata_q4_gemm_mfma_scratch(Nbig, K), &scr, stream);
+  if (rc) return rc;
+  rc = strata_q4_gemm_mfma_launch(x, Mf, K, big, nbig, y_dtype, scr, stream);
+  if (rc || Mf == M) return rc;
+  for (int i = 0; i < nbig; ++i) {
+    rc = strata_q4_gemm_launch(static_cast<const uint16_t*>(x) + (size_t)Mf * K, M - Mf, K,
+                               big[i].w, big[i].scales, big[i].biases, (int)big[i].N,
+                               static_cast<char*>(big[i].y) + (size_t)Mf * big[i].N * ye, y_dtype,
+                               stream);
+    if (rc) return rc;
+  }
+  return STRATA_OK;
+}
+
 int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t* w,
                    const uint16_t* s, const uint16_t* b, int N, void* y, int y_dtype,
                    void* stream) {
-  // Default: the hand-written kernels only (fused dequant, bf16 MFMA).
-  // STRATA_GEMM_LT_MIN_M > 0 opts into the dequantize + hipBLASLt path from
-  // that many rows (comparison runs only).
   const char* e = getenv("STRATA_GEMM_LT_MIN_M");
   const int min_rows = e ? atoi(e) : 0;
   if (min_rows <= 0 || M < min_rows || !aligned16(y)) {
-    // Full 256-row tiles on the 256 x 256 kernel, remaining rows (and any N
-    // that is not a multiple of 256) on the 128 x 128 kernel.
-    const int Mf = M / 256 * 256;
-    if (Mf >= kMfmaMinRows && N % 256 == 0 && aligned16(w)) {
-      void* scr = nullptr;
-      int rc = strata_ctx_scratch(ctx, strata_q4_gemm_mfma_scratch(N, K), &scr, stream);
-      if (rc) return rc;
-      rc = strata_q4_gemm_mfma_launch(x, Mf, K, w, s, b, N, y, y_dtype, scr, stream);
-      if (rc || Mf == M) return rc;
-      const size_t ye = y_dtype == STRATA_BF16 ? 2 : 4;
-      return strata_q4_gemm_launch(static_cast<const uint16_t*>(x) + (size_t)Mf * K, M - Mf, K,
-                                   w, s, b, N, static_cast<char*>(y) + (size_t)Mf * N * ye,
-                                   y_dtype, stream);
-    }
-    return strata_q4_gemm_launch(x, M, K, w, s, b, N, y, y_dtype, stream);
+    const strata_q4_weight wt{w, s, b, N, y};
+    return strata_q4_gemm_multi(ctx, x, M, K, &wt, 1, y_dtype, stream);
   }
   int rc = lt_init(ctx);
   if (rc) return rc;

@@ -31,7 +31,7 @@
 //     ~32 workgroups resident on one XCD share X and W tiles in its L2.
 #include <type_traits>
 
-#include "strata_common.h"
+#include "strata_internal.h"
 
 namespace {
 
@@ -115,11 +115,20 @@ struct Tile {
   static constexpr size_t kLds = (size_t)kStages * kStage;
 };
 
+// Outputs of the linears that share x, concatenated along N (each a
+// multiple of 256 columns): problem p owns columns n0[p] .. n0[p + 1] of
+// the re-laid-out weight and writes y[p] [M, n0[p + 1] - n0[p]].
+struct GemmOut {
+  void* y[kMaxGemmProblems];
+  int n0[kMaxGemmProblems + 1];
+  int count;
+};
+
 template <int TM, typename YT>
 __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(TM == 256 ? 1 : 2, TM == 256 ? 1 : 2)))
 void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
                          const uint32_t* __restrict__ wt, const uint32_t* __restrict__ sbt,
-                         int N, YT* __restrict__ y) {
+                         int N, GemmOut out) {
   constexpr int MB = Tile<TM>::MB, XCH = Tile<TM>::XCH, kXBytes = Tile<TM>::kXBytes;
   constexpr int kStage = Tile<TM>::kStage, kDmaPerStep = Tile<TM>::kDmaPerStep;
   constexpr int QPS = 8 / MB;  // dequant quarters per sub-step
@@ -308,15 +317,22 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 #endif
     stg = stg1;
   }
-  // C layout: lane holds column c32, rows 8 (i / 4) + 4 kh + i % 4.
-  YT* yb = y + (int64_t)(m0 + 4 * kh) * N + n0 + wave * WN + c32;
+  // C layout: lane holds column c32, rows 8 (i / 4) + 4 kh + i % 4.  The
+  // tile's problem (wave-uniform): the last one starting at or before n0.
+  int p = 0;
+#pragma unroll
+  for (int t = 1; t < kMaxGemmProblems; ++t)
+    if (t < out.count && n0 >= out.n0[t]) p = t;
+  const int np = out.n0[p + 1] - out.n0[p];
+  YT* yb = static_cast<YT*>(out.y[p]) + (int64_t)(m0 + 4 * kh) * np + (n0 - out.n0[p]) +
+           wave * WN + c32;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        Elem<YT>::store(yb, (int64_t)(mb * 32 + 8 * (i / 4) + i % 4) * N + nb * 32, acc[mb][nb][i]);
+        Elem<YT>::store(yb, (int64_t)(mb * 32 + 8 * (i / 4) + i % 4) * np + nb * 32, acc[mb][nb][i]);
 }
 
 // Re-layout of one q4 weight for the kernel above (a pass over the weight,
@@ -324,44 +340,62 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 // K step's rows are contiguous, each row's words in the order 0 2 4 6 | 1 3
 // 5 7 (halves swapped when bit 2 of n is set); scale and bias of (n, g)
 // packed in one word, sbt[g][n] = s | b << 16.
+// Rows 0 .. Np - 1 of one weight go to rows n_off .. of a layout Ntot rows
+// wide (the linears of one launch, concatenated).
 __global__ __launch_bounds__(256) void q4_gemm_relayout_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
-    int N, int G, uint4* __restrict__ wt, uint32_t* __restrict__ sbt) {
+    int Np, int G, int Ntot, int n_off, uint4* __restrict__ wt, uint32_t* __restrict__ sbt) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;  // (n, g), g fastest
-  if (i >= (int64_t)N * G) return;
-  const int n = (int)(i / G), g = (int)(i - (int64_t)n * G);
+  if (i >= (int64_t)Np * G) return;
+  const int nl = (int)(i / G), g = (int)(i - (int64_t)nl * G);
+  const int n = n_off + nl;
   const uint4 lo = w[i * 2], hi = w[i * 2 + 1];
   const uint4 ev = make_uint4(lo.x, lo.z, hi.x, hi.z), od = make_uint4(lo.y, lo.w, hi.y, hi.w);
   const int sw = (n >> 2) & 1;
-  wt[((int64_t)g * N + n) * 2 + sw] = ev;
-  wt[((int64_t)g * N + n) * 2 + (sw ^ 1)] = od;
-  sbt[(int64_t)g * N + n] = (uint32_t)s[i] | ((uint32_t)b[i] << 16);
+  wt[((int64_t)g * Ntot + n) * 2 + sw] = ev;
+  wt[((int64_t)g * Ntot + n) * 2 + (sw ^ 1)] = od;
+  sbt[(int64_t)g * Ntot + n] = (uint32_t)s[i] | ((uint32_t)b[i] << 16);
 }
 
 }  // namespace
 
-size_t strata_q4_gemm_mfma_scratch(int N, int K) {
+size_t strata_q4_gemm_mfma_scratch(int64_t N, int K) {
   return (size_t)N * K / 2 + (size_t)N * (K / TK) * 4;
 }
 
-int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const uint32_t* w, const uint16_t* s,
-                               const uint16_t* b, int N, void* y, int y_dtype, void* scratch,
-                               void* stream) {
+int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const strata_q4_weight* ws, int count,
+                               int y_dtype, void* scratch, void* stream) {
   STRATA_REQUIRE(K % TK == 0 && K >= TK, "q4 GEMM: K must be a positive multiple of 64");
-  STRATA_REQUIRE(M % 256 == 0 && N % TN == 0 && M > 0 && N > 0,
-                 "q4 GEMM (256-tile kernel): M and N must be positive multiples of 256");
+  STRATA_REQUIRE(count >= 1 && count <= kMaxGemmProblems, "q4 GEMM: 1..%d linears per launch",
+                 kMaxGemmProblems);
+  GemmOut out{};
+  out.count = count;
+  int N = 0;
+  for (int p = 0; p < count; ++p) {
+    STRATA_REQUIRE(ws[p].N > 0 && ws[p].N % TN == 0,
+                   "q4 GEMM (256-tile kernel): N must be a positive multiple of 256");
+    STRATA_REQUIRE((reinterpret_cast<uintptr_t>(ws[p].w) & 15) == 0, "q4 GEMM: unaligned weight");
+    out.y[p] = ws[p].y;
+    out.n0[p] = N;
+    N += (int)ws[p].N;
+  }
+  out.n0[count] = N;
+  STRATA_REQUIRE(M % 256 == 0 && M > 0, "q4 GEMM (256-tile kernel): M must be a positive multiple of 256");
   STRATA_REQUIRE((uint64_t)M * K * 2 < (1ull << 32) && (uint64_t)N * K / 2 < (1ull << 32),
                  "q4 GEMM (256-tile kernel): operands must be under 4 GiB");
-  STRATA_REQUIRE(scratch && ((reinterpret_cast<uintptr_t>(scratch) | reinterpret_cast<uintptr_t>(w)) & 15) == 0,
-                 "q4 GEMM: unaligned buffers");
+  STRATA_REQUIRE(scratch && (reinterpret_cast<uintptr_t>(scratch) & 15) == 0,
+                 "q4 GEMM: unaligned scratch");
   const int G = K / TK;
   uint32_t* wt = static_cast<uint32_t*>(scratch);
   uint32_t* sbt = wt + (size_t)N * K / 8;
-  const int64_t items = (int64_t)N * G;
-  hipLaunchKernelGGL(q4_gemm_relayout_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
-                     as_stream(stream), reinterpret_cast<const uint4*>(w), s, b, N, G,
-                     reinterpret_cast<uint4*>(wt), sbt);
-  STRATA_HIP_CHECK(hipGetLastError());
+  for (int p = 0; p < count; ++p) {
+    const int64_t items = (int64_t)ws[p].N * G;
+    hipLaunchKernelGGL(q4_gemm_relayout_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256),
+                       0, as_stream(stream), reinterpret_cast<const uint4*>(ws[p].w), ws[p].scales,
+                       ws[p].biases, (int)ws[p].N, G, N, out.n0[p], reinterpret_cast<uint4*>(wt),
+                       sbt);
+    STRATA_HIP_CHECK(hipGetLastError());
+  }
   // 256-row tiles unless that leaves the GPU under two workgroups per CU.
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess)
@@ -378,7 +412,7 @@ int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const uint32_t* w, c
     }                                                                                             \
     hipLaunchKernelGGL((q4_gemm_mfma_kernel<TMV, YT>), dim3((M / TMV) * (N / TN)), dim3(NTHR),    \
                        Tile<TMV>::kLds, as_stream(stream), (const uint16_t*)x, M, K, wt, sbt, N,  \
-                       (YT*)y);                                                                   \
+                       out);                                                                      \
   }
   if (y_dtype == STRATA_BF16) {
     if (big) STRATA_GEMM_GO(256, bf16_t) else STRATA_GEMM_GO(128, bf16_t)

@@ -37,9 +37,9 @@ int strata_bf16_gemv(strata_ctx* ctx, const void* x, int M, int K, const uint16_
                      void* y, int y_dtype, void* stream);
 int strata_q4_gemm_launch(const void* x, int M, int K, const uint32_t* w, const uint16_t* s,
                           const uint16_t* b, int N, void* y, int y_dtype, void* stream);
-// Prefill q4 linear (bf16 x, M > 8).  From STRATA_GEMM_LT_MIN_M rows on
-// (default 256) the weight is dequantized once into a bf16 tile owned by ctx
-// and multiplied with hipBLASLt; below it the fused-dequant MFMA kernel runs.
+// Prefill q4 linear (bf16 x, M > 8): the hand-written fused-dequant MFMA
+// kernels; STRATA_GEMM_LT_MIN_M > 0 opts into dequantize + hipBLASLt from
+// that many rows.
 int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t* w,
                    const uint16_t* s, const uint16_t* b, int N, void* y, int y_dtype,
                    void* stream);
@@ -48,10 +48,16 @@ void strata_gemm_lt_destroy(strata_ctx* ctx);
 constexpr int kMfmaMinRows = 256;
 // scratch: strata_q4_gemm_mfma_scratch(N, K) bytes, 16-byte aligned (the
 // weight's per-call re-layout).
-size_t strata_q4_gemm_mfma_scratch(int N, int K);
-int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const uint32_t* w, const uint16_t* s,
-                               const uint16_t* b, int N, void* y, int y_dtype, void* scratch,
-                               void* stream);
+size_t strata_q4_gemm_mfma_scratch(int64_t N, int K);
+// The linears of `ws` (same x; N of each a multiple of 256) in one launch of
+// the 256-column-tile kernel, full 256-row tiles only (M % 256 == 0).
+constexpr int kMaxGemmProblems = 8;
+int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const strata_q4_weight* ws, int count,
+                               int y_dtype, void* scratch, void* stream);
+// Prefill linears sharing x (M > 8 rows, bf16 x): one launch where the
+// shapes allow, else one per linear.
+int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
+                         int count, int y_dtype, void* stream);
 // bf16 [N, K] = s*q + b (fp32, one RNE rounding) of a q4 triple; K % 64 == 0,
 // w and out 16-byte aligned.
 int strata_q4_dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, int64_t N,

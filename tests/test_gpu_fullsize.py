@@ -83,3 +83,26 @@ def test_config5_layer_gemms_8k_sampled_rows(dev, name, N, K):
     yb = ops.linear(tx, tw, ts, tb)
     assert yb.dtype == torch.bfloat16
     assert rel_err(to_np_f32(yb)[rows], ref) < TOL_BF16
+
+
+def test_multi_linear_gemm_one_launch_equals_separate_launches(dev):
+    """q/k/v-shaped linears in one launch of the 256-tile kernel (weights
+    re-laid side by side, each tile writing its own output) against one
+    launch per linear; M = 8192 + 100 covers the remainder rows, and a
+    linear whose N is not a multiple of 256 takes the 128-tile kernel."""
+    from lokahi_amd import ops
+    M, K = 8192 + 100, 4096
+    g = torch.Generator(device=dev).manual_seed(6144)
+    ws = [ops.quantize(torch.randn((n, K), generator=g, device=dev) * 0.02)
+          for n in (4096, 1024, 1024, 1000)]
+    x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    fused = ops.linear_multi(x, ws)
+    for w, y in zip(ws, fused):
+        assert torch.equal(y, ops.linear(x, *w))
+    # the float64 oracle on rows of each problem, including remainder rows
+    from tests.gpu_util import bits
+    rows = np.array([0, 255, 256, 8191, 8192, 8291])
+    xr = bf16_bits_to_f32(bits(x[torch.from_numpy(rows).to(dev)]))
+    for (w, s, b), y in zip(ws, fused):
+        ref = q4.quantized_matmul(xr, bits(w), bits(s), bits(b))
+        assert rel_err(to_np_f32(y)[rows], ref) < TOL_BF16
