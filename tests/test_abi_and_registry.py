@@ -38,18 +38,23 @@ def test_loader_declares_signatures_and_fails_loudly_on_missing_library(tmp_path
 def test_registry_mirrors_reference_behaviour():
     from lokahi_amd.backends import (BackendError, HipBackend, get_backend, list_backends,
                                      register_backend, select_backend)
-    from lokahi_amd.backends.base import _parse_device_request
+    from lokahi_amd.backends.base import _route_device
     assert list_backends() == ("hip",)
     assert get_backend("hip").name == "hip"
-    assert _parse_device_request(None) == ("hip", None)
-    assert _parse_device_request("hip:0") == ("hip", "0")
-    assert _parse_device_request("cpu") == ("hip", "cpu")
+    assert _route_device(None) == ("hip", None)
+    assert _route_device("hip:0") == ("hip", "0")
+    assert _route_device("cpu") == ("hip", "cpu")
+    # base.py:83-105 semantics: a bare registered name, an empty device part,
+    # and an unregistered prefix kept whole as the default backend's request
+    assert _route_device("hip") == ("hip", None)
+    assert _route_device("hip:") == ("hip", None)
+    assert _route_device("cuda:1") == ("hip", "cuda:1")
     with pytest.raises(BackendError):
         register_backend(HipBackend())
     with pytest.raises(BackendError):
         get_backend("unknown")
     with pytest.raises(BackendError):
-        _parse_device_request(3)
+        _route_device(3)
     if not torch.cuda.is_available():
         # fail closed without a device
         assert not get_backend("hip").is_available()
