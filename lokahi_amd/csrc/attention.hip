@@ -22,6 +22,7 @@
 //   * attn_prefill_f32 : the same for fp32 inputs on 16x16x4 fp32 MFMA.
 //   * attn_generic : any other shape (e.g. tiny head dims), one wave per query.
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 
 #include "strata_common.h"
@@ -716,17 +717,28 @@ void attn_prefill_mfma32(
   float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = scale * kLog2e;
 
-  // LDS byte offsets inside a stage that do not change between tiles.
+  // This lane's LDS byte offsets inside a stage, fixed for the kernel: the
+  // swizzles depend only on the lane's part of the row index (32 kb and
+  // 16 s4 + 8 j leave fk and fv unchanged), so the per-tile and per-step
+  // parts are immediate offsets.
   // K operand of S^T block kb, step s: row 32 kb + c32, chunk 2s + h.
-  const int k_row_off = c32 * ROW;
-  const int k_swz = fk(c32);  // == fk(32 kb + c32)
+  int k_off[QS];
+#pragma unroll
+  for (int s = 0; s < QS; ++s) k_off[s] = c32 * ROW + 16 * ((2 * s + h) ^ fk(c32));
   // V^T operand (transpose read) of 16-key step s4, half j (keys 16 s4 + 8j
   // + 4h + 0..3) and head-dim block db: this lane addresses key
   // 16 s4 + 8j + 4h + (l' >> 2), head dims 32 db + 16 (g & 1) + 4 (l' & 3)
   // .. +3, g = lane / 16, l' = lane % 16.
   const int lp = lane & 15, g = lane >> 4;
-  const int v_key = 4 * h + (lp >> 2);      // plus 16 s4 + 8 j
+  const int v_key = 4 * h + (lp >> 2);            // plus 16 s4 + 8 j
   const int v_col = 16 * (g & 1) + 4 * (lp & 3);  // plus 32 db (elements)
+  int v_off[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    const int col = 32 * db + v_col;
+    v_off[db] = TILE + v_key * ROW + 16 * ((col / 8) ^ fv(v_key)) + 2 * (col % 8);
+  }
+  static_assert(NST == 2, "the tile loop alternates two stages");
 
   // Wait until at most n tiles' loads (2 NI each) of this thread are in flight.
   auto wait_tiles = [&](int n) {
@@ -741,12 +753,13 @@ void attn_prefill_mfma32(
   for (int t = 0; t < AHEAD && t < nt; ++t) issue(t * KT, t);
   wait_tiles(min(nt, AHEAD) - 1);
   __syncthreads();
-  int st = 0;
-  for (int t = 0; t < nt; ++t) {
+  // one tile on stage ST (a compile-time constant, so every LDS address is a
+  // lane offset plus an immediate)
+  auto tile = [&](int t, auto STC) {
+    constexpr int ST = decltype(STC)::value;
     const int kb0 = t * KT;
-    if (t + AHEAD < nt) issue((t + AHEAD) * KT, (t + AHEAD) % NST);  // the stage tile t - 1 used
-    const uint8_t* ks = lds + st * STAGE;
-    const uint8_t* vs = ks + TILE;
+    if (t + AHEAD < nt) issue((t + AHEAD) * KT, 1 - ST);  // the stage tile t - 1 used
+    const uint8_t* ks = lds + ST * STAGE;
     // Waves whose rows see no key of the tile skip its math (one scalar
     // branch); rows of a live wave that see none are masked to p = 0.
     if (__builtin_amdgcn_readfirstlane((int)(kb0 < wave_need))) {
@@ -761,8 +774,7 @@ void attn_prefill_mfma32(
       for (int s = 0; s < QS; ++s)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-          const uint4 a = *reinterpret_cast<const uint4*>(
-              ks + 32 * kb * ROW + k_row_off + 16 * ((2 * s + h) ^ k_swz));
+          const uint4 a = *reinterpret_cast<const uint4*>(ks + k_off[s] + 32 * kb * ROW);
           sc[kb] = mfma32_bf16(__builtin_bit_cast(bf16x8_t, a), qf[s], sc[kb]);
         }
       __builtin_amdgcn_s_setprio(0);
@@ -822,13 +834,10 @@ void attn_prefill_mfma32(
         for (int db = 0; db < DB; ++db) {
           v4i16_t vv[2];
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int key = 16 * s4 + 8 * j + v_key;
-            const int col = 32 * db + v_col;  // multiple of 4 elements
-            const int off = key * ROW + 16 * ((col / 8) ^ fv(key)) + 2 * (col % 8);
+          for (int j = 0; j < 2; ++j)
             vv[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) v4i16_t*)(lds0 + (uint32_t)(vs - lds) + off));
-          }
+                (__attribute__((address_space(3))) v4i16_t*)(lds0 + ST * STAGE + v_off[db] +
+                                                               (16 * s4 + 8 * j) * ROW));
           uint4 au;
           au.x = (uint16_t)vv[0][0] | ((uint32_t)(uint16_t)vv[0][1] << 16);
           au.y = (uint16_t)vv[0][2] | ((uint32_t)(uint16_t)vv[0][3] << 16);
@@ -843,7 +852,11 @@ void attn_prefill_mfma32(
     // flight), then in every thread
     wait_tiles(min(nt - 1, t + AHEAD) - (t + 1));
     __syncthreads();
-    st = st == NST - 1 ? 0 : st + 1;
+  };
+  for (int t = 0; t < nt; t += 2) {
+    tile(t, std::integral_constant<int, 0>{});
+    if (t + 1 >= nt) break;
+    tile(t + 1, std::integral_constant<int, 1>{});
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
