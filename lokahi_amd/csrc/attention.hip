@@ -14,7 +14,7 @@
 //     merges its lanes through LDS and writes (m, s, o[D]) partials;
 //     attn_decode_merge combines the chunks.
 //   * attn_prefill_mfma32 : Lq > 1, bf16 q/k/v, D in {64, 128}.  Flash-style
-//     on 32x32x16 MFMA: 64-key K and V tiles streamed straight from global
+//     on 32x32x16 MFMA: 32-key K and V tiles streamed straight from global
 //     memory into LDS (two stages), S^T = K Q^T and O^T += V^T P^T, every
 //     lane owns one query row and all softmax state is in-lane; V^T
 //     operands come from row-major V through the LDS transpose read.  Key
@@ -601,29 +601,28 @@ __device__ __forceinline__ f32x16_t mfma32_bf16(const bf16x8_t& a, const bf16x8_
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// bf16 prefill on 32x32x16 MFMA tiles.  Workgroup = 8 waves = 256 query
+// bf16 prefill on 32x32x16 MFMA tiles.  Workgroup = NW waves = 32 NW query
 // rows of one (b, query head) (grid order as prefill_item); wave w owns rows
-// qt*256 + 32w + 0..31.  S^T = K Q^T and O^T += V^T P^T run as 32x32x16
-// MFMAs whose 32-cycle issue leaves room for the other wave's softmax on the
+// qt*32NW + 32w + 0..31.  S^T = K Q^T and O^T += V^T P^T run as 32x32x16
+// MFMAs whose 32-cycle issue leaves room for other waves' softmax on the
 // SIMD; the P^T operand is the S^T accumulator itself (no shuffles).
-// K and V tiles (64 keys) are streamed by direct global -> LDS loads into a
-// ring of three stages, row-major with XOR-swizzled 16-byte chunks: the
-// loads of tile t + 2 are issued at the top of tile t, so two tiles of math
-// cover their latency, and no register holds them.  V^T operands come from
-// row-major V through the LDS transpose read (ds_read_b64_tr_b16: in each
-// 16-lane group, lane l' receives element (l' & 3) of the 4-element rows
-// addressed by lanes 4k + (l' >> 2), k < 4).
+// K and V tiles (KT keys) are streamed by direct global -> LDS loads into a
+// ring of NST stages, row-major with XOR-swizzled 16-byte chunks: the loads
+// of tile t + NST - 1 are issued at the top of tile t, and no register holds
+// them.  V^T operands come from row-major V through the LDS transpose read
+// (ds_read_b64_tr_b16: in each 16-lane group, lane l' receives element
+// (l' & 3) of the 4-element rows addressed by lanes 4k + (l' >> 2), k < 4).
 // MFMA 32x32x16 layouts (wave64): A (32 x 16): lane l holds row l%32, k
 // 8(l/32) .. +8; B (16 x 32): lane l holds column l%32, the same k; C (32 x
 // 32): lane l holds column l%32, rows 8(i/4) + 4(l/32) + i%4 for i < 16.
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
-template <int D, int NW, int NST>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+template <int D, int NW, int NST, int KT>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(KT == 32 ? 3 : 2)))
 void attn_prefill_mfma32(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int B, int Hq, int Hkv,
     int Lq, int Lk, int causal, float scale, float eps, int out_tm, bf16_t* __restrict__ out) {
-  constexpr int KT = 64;              // keys per tile
+  constexpr int KB = KT / 32;         // 32-key score blocks per tile
   constexpr int ROW = D * 2;          // bytes per K / V row
   constexpr int NCHK = D / 8;         // 16-byte chunks per row
   constexpr int TILE = KT * ROW;      // bytes of one K or V tile
@@ -738,7 +737,7 @@ void attn_prefill_mfma32(
     const int col = 32 * db + v_col;
     v_off[db] = TILE + v_key * ROW + 16 * ((col / 8) ^ fv(v_key)) + 2 * (col % 8);
   }
-  static_assert(NST == 2, "the tile loop alternates two stages");
+  static_assert(NST == 2 || NST == 3, "the tile loop cycles two or three stages");
 
   // Wait until at most n tiles' loads (2 NI each) of this thread are in flight.
   auto wait_tiles = [&](int n) {
@@ -758,22 +757,22 @@ void attn_prefill_mfma32(
   auto tile = [&](int t, auto STC) {
     constexpr int ST = decltype(STC)::value;
     const int kb0 = t * KT;
-    if (t + AHEAD < nt) issue((t + AHEAD) * KT, 1 - ST);  // the stage tile t - 1 used
+    if (t + AHEAD < nt) issue((t + AHEAD) * KT, (ST + AHEAD) % NST);  // the stage tile t - 1 used
     const uint8_t* ks = lds + ST * STAGE;
     // Waves whose rows see no key of the tile skip its math (one scalar
     // branch); rows of a live wave that see none are masked to p = 0.
     if (__builtin_amdgcn_readfirstlane((int)(kb0 < wave_need))) {
       __builtin_amdgcn_s_setprio(1);
       // st[kb][i] = score(this lane's row, key kb0 + 32 kb + 8(i/4) + 4h + i%4)
-      f32x16_t sc[2];
+      f32x16_t sc[KB];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[kb][r] = 0.f;
 #pragma unroll
       for (int s = 0; s < QS; ++s)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < KB; ++kb) {
           const uint4 a = *reinterpret_cast<const uint4*>(ks + k_off[s] + 32 * kb * ROW);
           sc[kb] = mfma32_bf16(__builtin_bit_cast(bf16x8_t, a), qf[s], sc[kb]);
         }
@@ -782,7 +781,7 @@ void attn_prefill_mfma32(
       // folded into the exponent's FMA, sl2 > 0)
       if (kb0 + KT > kfull) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int key = kb0 + 32 * kb + 8 * (i / 4) + 4 * h + i % 4;
@@ -792,7 +791,7 @@ void attn_prefill_mfma32(
       }
       float mb = -INFINITY;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) mb = fmaxf(mb, sc[kb][i]);
       mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
@@ -803,7 +802,7 @@ void attn_prefill_mfma32(
       const float nmn = none ? 0.f : -mn;
       float ps = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const float p = __builtin_amdgcn_exp2f(fmaf(sc[kb][i], sl2, nmn));  // exp2(-inf) = 0
@@ -853,10 +852,14 @@ void attn_prefill_mfma32(
     wait_tiles(min(nt - 1, t + AHEAD) - (t + 1));
     __syncthreads();
   };
-  for (int t = 0; t < nt; t += 2) {
+  for (int t = 0; t < nt; t += NST) {
     tile(t, std::integral_constant<int, 0>{});
     if (t + 1 >= nt) break;
     tile(t + 1, std::integral_constant<int, 1>{});
+    if constexpr (NST == 3) {
+      if (t + 2 >= nt) break;
+      tile(t + 2, std::integral_constant<int, 2 % NST>{});
+    }
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
@@ -1048,18 +1051,20 @@ int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v,
   if constexpr (sizeof(TQ) == sizeof(TK) && sizeof(TK) == sizeof(TV)) {
     if (Lq > 1 && (D == 64 || D == 128)) {
       if constexpr (sizeof(TQ) == 2) {
-        // 4 waves (128 query rows) per workgroup, two LDS stages: two
-        // workgroups per CU, whose waves share each SIMD without sharing a
-        // barrier (8k causal: 635 us; 8 waves with 3 or 4 stages in one
-        // workgroup per CU: 685-696 us)
-        constexpr int NWV = 4, NSTV = 2;
+        // 4 waves (128 query rows) per workgroup, two LDS stages of 32-key
+        // tiles (32 KB): three workgroups per CU (160 VGPRs), whose waves
+        // share each SIMD without sharing a barrier (8k causal: 586-602 us;
+        // 64-key tiles, two workgroups per CU: 606-628 us; 8 waves in one
+        // workgroup per CU: 683-696 us; a third stage: no gain)
+        constexpr int NWV = 4, NSTV = 2, KTV = 32;
         const dim3 grid(prefill_grid((Lq + 32 * NWV - 1) / (32 * NWV), B, Hkv, Hq / Hkv));
         if (D == 64)
-          hipLaunchKernelGGL((attn_prefill_mfma32<64, NWV, NSTV>), grid, dim3(64 * NWV), 0, stream,
-                             (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, kv_bs, kv_hs,
-                             qpos, B, Hq, Hkv, Lq, Lk, causal, scale, eps, ex.out_tm, (bf16_t*)out);
+          hipLaunchKernelGGL((attn_prefill_mfma32<64, NWV, NSTV, KTV>), grid, dim3(64 * NWV), 0,
+                             stream, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, kv_bs,
+                             kv_hs, qpos, B, Hq, Hkv, Lq, Lk, causal, scale, eps, ex.out_tm,
+                             (bf16_t*)out);
         else
-          hipLaunchKernelGGL((attn_prefill_mfma32<128, NWV, NSTV>), grid, dim3(64 * NWV), 0,
+          hipLaunchKernelGGL((attn_prefill_mfma32<128, NWV, NSTV, KTV>), grid, dim3(64 * NWV), 0,
                              stream, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, kv_bs,
                              kv_hs, qpos, B, Hq, Hkv, Lq, Lk, causal, scale, eps, ex.out_tm,
                              (bf16_t*)out);
