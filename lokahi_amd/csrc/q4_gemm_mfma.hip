@@ -132,6 +132,11 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   constexpr int MB = Tile<TM>::MB, XCH = Tile<TM>::XCH, kXBytes = Tile<TM>::kXBytes;
   constexpr int kStage = Tile<TM>::kStage, kDmaPerStep = Tile<TM>::kDmaPerStep;
   constexpr int QPS = 8 / MB;  // dequant quarters per sub-step
+  // Sub-step that reads step g + 1's code words and scales (after this
+  // lane's loads of step g + 1 are waited for, which needs every load of
+  // step g + 2 issued first).
+  constexpr int kReadSt = 3 * MB - 4;
+  static_assert(kReadSt - 1 >= kDmaPerStep - 1, "the load wait must follow step g + 2's issue");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int mt = M / TM, nt = N / TN;
   int tmi, tni;
@@ -203,23 +208,23 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   // step g + 1 in the k block after its last use (k block 3 of step g + 1
   // during k block 0 of step g + 1).
   uint4 bf[NB][KB];
-  uint4 dw[NB];
+  // dw / dsf, dbf: code words, scales and biases of the step being
+  // dequantized; dwn / dsbn: the next step's words and (s | b << 16), read
+  // ahead of their first use.
+  uint4 dw[NB], dwn[NB];
   float dsf[NB], dbf[NB];
-  auto read_sb = [&](int stg) {
+  uint32_t dsbn[NB];
+  auto read_sb = [&](int stg, uint32_t (&o)[NB]) {
     const uint8_t* ss = lds + stg * kStage + kXBytes + kWBytes + wave * 256;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const uint32_t v = *reinterpret_cast<const uint32_t*>(ss + (nb * 32 + c32) * 4);
-      dsf[nb] = __uint_as_float(v << 16);
-      dbf[nb] = __uint_as_float(v & 0xffff0000u);
-    }
+    for (int nb = 0; nb < NB; ++nb) o[nb] = *reinterpret_cast<const uint32_t*>(ss + (nb * 32 + c32) * 4);
   };
-  auto read_w = [&](int stg) {
+  auto read_w = [&](int stg, uint4 (&o)[NB]) {
     const uint8_t* ws = lds + stg * kStage + kXBytes + wave * 2048;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
-      dw[nb] = *reinterpret_cast<const uint4*>(ws + (nb * 32 + c32) * 32 +
-                                               ((kh ^ ((c32 >> 2) & 1)) << 4));
+      o[nb] = *reinterpret_cast<const uint4*>(ws + (nb * 32 + c32) * 32 +
+                                              ((kh ^ ((c32 >> 2) & 1)) << 4));
   };
   // quarter q of the word of fragment nb: output register q (codes 2q, 2q+1)
   uint32_t dlo[NB], dhi[NB];
@@ -258,8 +263,13 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   issue(min(1, G - 1), 1);
   vm_wait_step();
   __syncthreads();
-  read_sb(0);
-  read_w(0);
+  read_sb(0, dsbn);
+  read_w(0, dw);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    dsf[nb] = __uint_as_float(dsbn[nb] << 16);
+    dbf[nb] = __uint_as_float(dsbn[nb] & 0xffff0000u);
+  }
   dequant_all(0);
 
   // One K step = 32 sub-steps (k block kblk = st / 8, row block mb = st % 8),
@@ -284,23 +294,32 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
     const int gn = min(g + 2, G - 1);
     const uint8_t* xb = lds + stg * kStage;
     uint4 a = *reinterpret_cast<const uint4*>(xb + aoff(0, 0));
+    uint4 an = *reinterpret_cast<const uint4*>(xb + aoff(1 % MB, 1 / MB));
 #pragma unroll
     for (int st = 0; st < KB * MB; ++st) {
       const int kblk = st / MB, mb = st % MB;
-      uint4 an = a;
-      if (st + 1 < KB * MB)
-        an = *reinterpret_cast<const uint4*>(xb + aoff((st + 1) % MB, (st + 1) / MB));
+      uint4 ann = an;
+      if (st + 2 < KB * MB)
+        ann = *reinterpret_cast<const uint4*>(xb + aoff((st + 2) % MB, (st + 2) / MB));
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32(a, bf[nb][kblk], acc[mb][nb]);
 #ifndef GEMM_EXP_NO_DMA
       if (st < kDmaPerStep) issue1(gn, stg2, st);
 #endif
 #ifndef GEMM_EXP_NO_WAIT
-      if (st == 3 * MB - 1) vm_wait_step();
+      if (st == kReadSt - 1) vm_wait_step();
 #endif
-      if (st == 3 * MB) {
-        read_sb(stg1);  // step g's last dequant was one sub-step earlier
-        read_w(stg1);
+      if (st == kReadSt) {  // step g + 1's words, four sub-steps before their first use
+        read_sb(stg1, dsbn);
+        read_w(stg1, dwn);
+      }
+      if (st == 3 * MB) {  // step g's last dequant was one sub-step earlier
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          dw[nb] = dwn[nb];
+          dsf[nb] = __uint_as_float(dsbn[nb] << 16);
+          dbf[nb] = __uint_as_float(dsbn[nb] & 0xffff0000u);
+        }
       }
 #ifndef GEMM_EXP_NO_DEQ
 #pragma unroll
@@ -311,6 +330,7 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 #endif
       __builtin_amdgcn_sched_barrier(0);
       a = an;
+      an = ann;
     }
 #ifndef GEMM_EXP_NO_BAR
     __syncthreads();
