@@ -361,13 +361,18 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 // 5 7 (halves swapped when bit 2 of n is set); scale and bias of (n, g)
 // packed in one word, sbt[g][n] = s | b << 16.
 // Rows 0 .. Np - 1 of one weight go to rows n_off .. of a layout Ntot rows
-// wide (the linears of one launch, concatenated).
+// wide (the linears of one launch, concatenated).  A workgroup moves a tile
+// of 32 rows x 8 groups: thread t takes row t / 8 and group t % 8, so the
+// reads (8 groups of a row, 256 contiguous bytes) and the writes (8 rows of
+// a group, 256 contiguous bytes) both run in 256-byte pieces.
 __global__ __launch_bounds__(256) void q4_gemm_relayout_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
     int Np, int G, int Ntot, int n_off, uint4* __restrict__ wt, uint32_t* __restrict__ sbt) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;  // (n, g), g fastest
-  if (i >= (int64_t)Np * G) return;
-  const int nl = (int)(i / G), g = (int)(i - (int64_t)nl * G);
+  const int gtiles = (G + 7) / 8;
+  const int nt = blockIdx.x / gtiles, gt = blockIdx.x - nt * gtiles;
+  const int nl = nt * 32 + (threadIdx.x >> 3), g = gt * 8 + (threadIdx.x & 7);
+  if (nl >= Np || g >= G) return;
+  const int64_t i = (int64_t)nl * G + g;  // (row, group) of the source
   const int n = n_off + nl;
   const uint4 lo = w[i * 2], hi = w[i * 2 + 1];
   const uint4 ev = make_uint4(lo.x, lo.z, hi.x, hi.z), od = make_uint4(lo.y, lo.w, hi.y, hi.w);
@@ -409,8 +414,8 @@ int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const strata_q4_weig
   uint32_t* wt = static_cast<uint32_t*>(scratch);
   uint32_t* sbt = wt + (size_t)N * K / 8;
   for (int p = 0; p < count; ++p) {
-    const int64_t items = (int64_t)ws[p].N * G;
-    hipLaunchKernelGGL(q4_gemm_relayout_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256),
+    const int64_t tiles = (ws[p].N + 31) / 32 * ((G + 7) / 8);
+    hipLaunchKernelGGL(q4_gemm_relayout_kernel, dim3((unsigned)tiles), dim3(256),
                        0, as_stream(stream), reinterpret_cast<const uint4*>(ws[p].w), ws[p].scales,
                        ws[p].biases, (int)ws[p].N, G, N, out.n0[p], reinterpret_cast<uint4*>(wt),
                        sbt);
