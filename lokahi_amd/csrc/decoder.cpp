@@ -57,6 +57,9 @@ struct strata_decoder {
   std::map<int, hipGraphExec_t> graphs;
   int graph_batch;
   float graph_temp;
+  // Prefill GEMM layout of each layer's launches (q/k/v, o, gate/up, down),
+  // re-laid out once at creation (null: re-laid out per call).
+  std::vector<void*> packed;
 };
 
 namespace {
@@ -158,7 +161,8 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
     qkv[2].y = d->v;
     void* kc = kv->kl(li);
     void* vc = kv->vl(li);
-    RC(strata_q4_gemm_multi(d->ctx, d->xn, T, H, qkv, 3, STRATA_BF16, stream));
+    const void* const* pk = d->packed.empty() ? nullptr : &d->packed[(size_t)li * 4];
+    RC(strata_q4_gemm_multi(d->ctx, d->xn, T, H, qkv, 3, STRATA_BF16, stream, pk ? pk[0] : nullptr));
     RC(strata_rope_kv_fused_launch(d->q, d->k, d->v, STRATA_BF16, B, Hq, Hkv, L, D, kv->Lmax,
                                    pos0, nullptr, c.rope_theta, d->qr, kc, vc, STRATA_BF16,
                                    stream));
@@ -169,18 +173,18 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
                                  d->attn, ex, stream));
     strata_q4_weight o = Lw.o;
     o.y = d->o;
-    RC(strata_q4_gemm(d->ctx, d->attn, T, Hq * D, o.w, o.scales, o.biases, (int)o.N, o.y,
-                             STRATA_BF16, stream));
+    RC(strata_q4_gemm_multi(d->ctx, d->attn, T, Hq * D, &o, 1, STRATA_BF16, stream,
+                            pk ? pk[1] : nullptr));
     RC(strata_rmsnorm_launch(d->h, d->o, Lw.post_norm, T, H, c.rms_norm_eps, d->xn, stream));
     strata_q4_weight gu[2] = {Lw.gate, Lw.up};
     gu[0].y = d->gate;
     gu[1].y = d->up;
-    RC(strata_q4_gemm_multi(d->ctx, d->xn, T, H, gu, 2, STRATA_BF16, stream));
+    RC(strata_q4_gemm_multi(d->ctx, d->xn, T, H, gu, 2, STRATA_BF16, stream, pk ? pk[2] : nullptr));
     RC(strata_silu_mul_launch(d->gate, d->up, (int64_t)T * F, d->act, stream));
     strata_q4_weight dn = Lw.down;
     dn.y = d->delta;
-    RC(strata_q4_gemm(d->ctx, d->act, T, F, dn.w, dn.scales, dn.biases, (int)dn.N, dn.y,
-                             STRATA_BF16, stream));
+    RC(strata_q4_gemm_multi(d->ctx, d->act, T, F, &dn, 1, STRATA_BF16, stream,
+                            pk ? pk[3] : nullptr));
   }
   // final norm of h + delta, then lm_head on the last position of each row
   RC(strata_rmsnorm_launch(d->h, d->delta, d->final_norm, T, H, c.rms_norm_eps, d->hn, stream));
@@ -217,6 +221,47 @@ int check_forward(strata_decoder* d, int B, int L) {
 
 void set_lengths(strata_decoder* d, int len) {
   for (int& l : d->kv->len) l = len;
+}
+
+// Load-time re-layout of the prefill weights (the MLX layout stays the
+// interchange and decode format): for each layer the four GEMM launches of a
+// prefill, in the layout of q4_gemm_relayout_kernel, when prefills can reach
+// the 256-row kernel and every linear qualifies.  Costs one more copy of the
+// q4 linears; on an allocation failure the prefill re-lays out per call.
+int pack_prefill_weights(strata_decoder* d) {
+  const strata_llama_config& c = d->cfg;
+  if (d->max_tokens < kMfmaMinRows) return STRATA_OK;
+  const int H = c.hidden_size, F = c.intermediate_size, QW = c.num_heads * c.head_dim;
+  std::vector<void*> packed;
+  for (const strata_llama_layer& L : d->layers) {
+    const strata_q4_weight groups[4][3] = {{L.q, L.k, L.v}, {L.o}, {L.gate, L.up}, {L.down}};
+    const int counts[4] = {3, 1, 2, 1}, Ks[4] = {H, QW, H, F};
+    for (int gi = 0; gi < 4; ++gi) {
+      int64_t N = 0;
+      for (int i = 0; i < counts[gi]; ++i) {
+        const strata_q4_weight& w = groups[gi][i];
+        if (w.N % 256 != 0 || !aligned16(w.w)) {
+          for (void* p : packed) hipFree(p);
+          return STRATA_OK;  // this model's prefill re-lays out per call
+        }
+        N += w.N;
+      }
+      void* p = nullptr;
+      if (hipMalloc(&p, strata_q4_gemm_mfma_scratch(N, Ks[gi])) != hipSuccess) {
+        (void)hipGetLastError();
+        for (void* q : packed) hipFree(q);
+        return STRATA_OK;
+      }
+      packed.push_back(p);
+      const int rc = strata_q4_gemm_pack(groups[gi], counts[gi], Ks[gi], p, nullptr);
+      if (rc) {
+        for (void* q : packed) hipFree(q);
+        return rc;
+      }
+    }
+  }
+  d->packed.swap(packed);
+  return STRATA_OK;
 }
 
 }  // namespace
@@ -279,6 +324,7 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
   if (!rc)
     rc = alloc(reinterpret_cast<void**>(&d->part),
                (size_t)kv->B * c.num_heads * part_stride(d->part_splits, c.head_dim) * 4);
+  if (!rc) rc = pack_prefill_weights(d);
   if (!rc) rc = strata_rope_table_launch(d->rope_table, kv->Lmax, c.head_dim, c.rope_theta, nullptr);
   if (!rc && hipDeviceSynchronize() != hipSuccess)
     rc = strata_set_error(STRATA_EHIP, "decoder: RoPE table initialisation failed");
@@ -296,6 +342,7 @@ int strata_decoder_destroy(strata_decoder* d) {
   if (!d) return STRATA_OK;
   hipDeviceSynchronize();
   for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
+  for (void* p : d->packed) hipFree(p);
   void* ptrs[] = {d->h, d->xn, d->q, d->k, d->v, d->qr, d->attn, d->o, d->gate, d->up, d->act,
                   d->delta, d->hn, d->logits, d->ids, d->tokens, d->counters, d->part, d->amax,
                   d->rope_table, d->rope_cur};
@@ -315,6 +362,7 @@ int strata_decoder_set_lm_head_q4(strata_decoder* d, const strata_q4_weight* hea
   // captured decode steps hold the previous head
   STRATA_HIP_CHECK(hipStreamSynchronize(d->stream));
   for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
+  for (void* p : d->packed) hipFree(p);
   d->graphs.clear();
   d->head_q4 = *head;
   d->head_q4.y = nullptr;

@@ -185,7 +185,7 @@ void strata_gemm_lt_destroy(strata_ctx* ctx) {
 }
 
 int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
-                         int count, int y_dtype, void* stream) {
+                         int count, int y_dtype, void* stream, const void* packed) {
   // Default: the hand-written kernels only (fused dequant, bf16 MFMA):
   // full 256-row tiles of every linear in one launch of the 256 x 256
   // kernel, remaining rows (and linears whose N is not a multiple of 256)
@@ -219,10 +219,15 @@ int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const str
     }
   }
   if (nbig == 0) return STRATA_OK;
-  void* scr = nullptr;
-  int rc = strata_ctx_scratch(ctx, strata_q4_gemm_mfma_scratch(Nbig, K), &scr, stream);
-  if (rc) return rc;
-  rc = strata_q4_gemm_mfma_launch(x, Mf, K, big, nbig, y_dtype, scr, stream);
+  int rc;
+  if (packed && nbig == count) {  // weights re-laid out at load time, in this order
+    rc = strata_q4_gemm_mfma_run(x, Mf, K, packed, big, nbig, y_dtype, stream);
+  } else {
+    void* scr = nullptr;
+    rc = strata_ctx_scratch(ctx, strata_q4_gemm_mfma_scratch(Nbig, K), &scr, stream);
+    if (rc) return rc;
+    rc = strata_q4_gemm_mfma_launch(x, Mf, K, big, nbig, y_dtype, scr, stream);
+  }
   if (rc || Mf == M) return rc;
   for (int i = 0; i < nbig; ++i) {
     rc = strata_q4_gemm_launch(static_cast<const uint16_t*>(x) + (size_t)Mf * K, M - Mf, K,

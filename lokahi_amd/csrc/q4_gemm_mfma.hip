@@ -384,43 +384,78 @@ __global__ __launch_bounds__(256) void q4_gemm_relayout_kernel(
 
 }  // namespace
 
-size_t strata_q4_gemm_mfma_scratch(int64_t N, int K) {
+size_t strata_q4_gemm_mfma_scratch(int64_t N, int K) {  // == strata_q4_gemm_pack's buffer
   return (size_t)N * K / 2 + (size_t)N * (K / TK) * 4;
 }
 
-int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const strata_q4_weight* ws, int count,
-                               int y_dtype, void* scratch, void* stream) {
-  STRATA_REQUIRE(K % TK == 0 && K >= TK, "q4 GEMM: K must be a positive multiple of 64");
+namespace {
+// Checks the linears of one launch and fills their output table; returns the
+// concatenated N through *Ntot.
+int gemm_problems(const strata_q4_weight* ws, int count, GemmOut* out, int* Ntot) {
   STRATA_REQUIRE(count >= 1 && count <= kMaxGemmProblems, "q4 GEMM: 1..%d linears per launch",
                  kMaxGemmProblems);
-  GemmOut out{};
-  out.count = count;
-  int N = 0;
+  *out = GemmOut{};
+  out->count = count;
+  int64_t N = 0;
   for (int p = 0; p < count; ++p) {
     STRATA_REQUIRE(ws[p].N > 0 && ws[p].N % TN == 0,
                    "q4 GEMM (256-tile kernel): N must be a positive multiple of 256");
-    STRATA_REQUIRE((reinterpret_cast<uintptr_t>(ws[p].w) & 15) == 0, "q4 GEMM: unaligned weight");
-    out.y[p] = ws[p].y;
-    out.n0[p] = N;
-    N += (int)ws[p].N;
+    out->y[p] = ws[p].y;
+    out->n0[p] = (int)N;
+    N += ws[p].N;
   }
-  out.n0[count] = N;
-  STRATA_REQUIRE(M % 256 == 0 && M > 0, "q4 GEMM (256-tile kernel): M must be a positive multiple of 256");
-  STRATA_REQUIRE((uint64_t)M * K * 2 < (1ull << 32) && (uint64_t)N * K / 2 < (1ull << 32),
-                 "q4 GEMM (256-tile kernel): operands must be under 4 GiB");
-  STRATA_REQUIRE(scratch && (reinterpret_cast<uintptr_t>(scratch) & 15) == 0,
-                 "q4 GEMM: unaligned scratch");
+  STRATA_REQUIRE(N <= INT32_MAX, "q4 GEMM: too many output columns");
+  out->n0[count] = (int)N;
+  *Ntot = (int)N;
+  return STRATA_OK;
+}
+}  // namespace
+
+int strata_q4_gemm_pack(const strata_q4_weight* ws, int count, int K, void* packed, void* stream) {
+  STRATA_REQUIRE(K % TK == 0 && K >= TK, "q4 GEMM: K must be a positive multiple of 64");
+  GemmOut out;
+  int N = 0;
+  int rc = gemm_problems(ws, count, &out, &N);
+  if (rc) return rc;
+  STRATA_REQUIRE((uint64_t)N * K / 2 < (1ull << 32), "q4 GEMM (256-tile kernel): weight over 4 GiB");
+  STRATA_REQUIRE(packed && (reinterpret_cast<uintptr_t>(packed) & 15) == 0,
+                 "q4 GEMM: unaligned packed buffer");
   const int G = K / TK;
-  uint32_t* wt = static_cast<uint32_t*>(scratch);
+  uint32_t* wt = static_cast<uint32_t*>(packed);
   uint32_t* sbt = wt + (size_t)N * K / 8;
   for (int p = 0; p < count; ++p) {
+    STRATA_REQUIRE((reinterpret_cast<uintptr_t>(ws[p].w) & 15) == 0, "q4 GEMM: unaligned weight");
     const int64_t tiles = (ws[p].N + 31) / 32 * ((G + 7) / 8);
-    hipLaunchKernelGGL(q4_gemm_relayout_kernel, dim3((unsigned)tiles), dim3(256),
-                       0, as_stream(stream), reinterpret_cast<const uint4*>(ws[p].w), ws[p].scales,
+    hipLaunchKernelGGL(q4_gemm_relayout_kernel, dim3((unsigned)tiles), dim3(256), 0,
+                       as_stream(stream), reinterpret_cast<const uint4*>(ws[p].w), ws[p].scales,
                        ws[p].biases, (int)ws[p].N, G, N, out.n0[p], reinterpret_cast<uint4*>(wt),
                        sbt);
     STRATA_HIP_CHECK(hipGetLastError());
   }
+  return STRATA_OK;
+}
+
+int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const strata_q4_weight* ws, int count,
+                               int y_dtype, void* scratch, void* stream) {
+  const int rc = strata_q4_gemm_pack(ws, count, K, scratch, stream);
+  if (rc) return rc;
+  return strata_q4_gemm_mfma_run(x, M, K, scratch, ws, count, y_dtype, stream);
+}
+
+int strata_q4_gemm_mfma_run(const void* x, int M, int K, const void* packed,
+                            const strata_q4_weight* ws, int count, int y_dtype, void* stream) {
+  STRATA_REQUIRE(K % TK == 0 && K >= TK, "q4 GEMM: K must be a positive multiple of 64");
+  GemmOut out;
+  int N = 0;
+  int rc = gemm_problems(ws, count, &out, &N);
+  if (rc) return rc;
+  STRATA_REQUIRE(M % 256 == 0 && M > 0, "q4 GEMM (256-tile kernel): M must be a positive multiple of 256");
+  STRATA_REQUIRE((uint64_t)M * K * 2 < (1ull << 32) && (uint64_t)N * K / 2 < (1ull << 32),
+                 "q4 GEMM (256-tile kernel): operands must be under 4 GiB");
+  STRATA_REQUIRE(packed && (reinterpret_cast<uintptr_t>(packed) & 15) == 0,
+                 "q4 GEMM: unaligned packed buffer");
+  const uint32_t* wt = static_cast<const uint32_t*>(packed);
+  const uint32_t* sbt = wt + (size_t)N * K / 8;
   // 256-row tiles unless that leaves the GPU under two workgroups per CU.
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess)

@@ -54,10 +54,17 @@ size_t strata_q4_gemm_mfma_scratch(int64_t N, int K);
 constexpr int kMaxGemmProblems = 8;
 int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const strata_q4_weight* ws, int count,
                                int y_dtype, void* scratch, void* stream);
+// The same in two parts: the weights' re-layout into `packed`
+// (strata_q4_gemm_mfma_scratch(sum of N, K) bytes, 16-byte aligned; done
+// once at load time by the decoder), then GEMMs on it (the ws' w, scales and
+// biases are not read, only N and y).
+int strata_q4_gemm_pack(const strata_q4_weight* ws, int count, int K, void* packed, void* stream);
+int strata_q4_gemm_mfma_run(const void* x, int M, int K, const void* packed,
+                            const strata_q4_weight* ws, int count, int y_dtype, void* stream);
 // Prefill linears sharing x (M > 8 rows, bf16 x): one launch where the
 // shapes allow, else one per linear.
 int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
-                         int count, int y_dtype, void* stream);
+                         int count, int y_dtype, void* stream, const void* packed = nullptr);
 // bf16 [N, K] = s*q + b (fp32, one RNE rounding) of a q4 triple; K % 64 == 0,
 // w and out 16-byte aligned.
 int strata_q4_dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, int64_t N,
