@@ -141,6 +141,34 @@ def test_config5_prefill_bf16_mfma(dev, L, chunk):
     assert rel_err(to_np_f32(out), ref) < TOL_BF16
 
 
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 8, 2), (128, 12, 4), (64, 24, 8)])
+def test_prefill_bf16_mfma32_ragged_positions_and_non_causal(dev, D, Hq, Hkv):
+    """The bf16 32x32x16 prefill kernel off the bench geometry: head dims 64
+    and 128, groups 4 and 3, batch 2, queries at explicit positions over a
+    longer key range (32-key tiles with a tail, rows past Lq in the last
+    128-row tile), and the non-causal form, against the float64 oracle."""
+    from lokahi_amd import ops
+    rng = np.random.default_rng(D * 100 + Hq)
+    B, Lq, Lk = 2, 70, 150
+    q = round_bf16(rng.normal(size=(B, Hq, Lq, D)).astype(np.float32))
+    k = round_bf16(rng.normal(size=(B, Hkv, Lk, D)).astype(np.float32))
+    v = round_bf16(rng.normal(size=(B, Hkv, Lk, D)).astype(np.float32))
+    pos = np.stack([np.arange(Lk - Lq, Lk), np.sort(rng.integers(0, Lk, Lq))])
+    tq, tk, tv = bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev)
+    out = ops.attention(tq, tk, tv, query_positions=_t(pos, dev))
+    assert rel_err(to_np_f32(out), att.naive_gqa(q, k, v, pos)) < TOL_BF16
+    nm = ops.attention(tq, tk, tv, causal=False)
+    assert rel_err(to_np_f32(nm), att.naive_gqa(q, k, v)) < TOL_BF16
+    # bottom-right causal over Lq = Lk = 300 (several tiles, a partial last one)
+    L = 300
+    q2 = round_bf16(rng.normal(size=(1, Hq, L, D)).astype(np.float32))
+    k2 = round_bf16(rng.normal(size=(1, Hkv, L, D)).astype(np.float32))
+    v2 = round_bf16(rng.normal(size=(1, Hkv, L, D)).astype(np.float32))
+    o2 = ops.attention(bf16_dev(q2, dev), bf16_dev(k2, dev), bf16_dev(v2, dev))
+    ref2 = att.naive_gqa(q2, k2, v2, np.arange(L)[None])  # positions: causal
+    assert rel_err(to_np_f32(o2), ref2) < TOL_BF16
+
+
 def test_prefill_fp32_mfma_ragged_and_positions(dev):
     from lokahi_amd import ops
     rng = np.random.default_rng(77)
