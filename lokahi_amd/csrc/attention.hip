@@ -360,10 +360,10 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict
     mx = mb;
   }
   // lanes t and t+32 of a wave hold the same columns
-  acc.x += __shfl_xor(acc.x, 32, 64);
-  acc.y += __shfl_xor(acc.y, 32, 64);
-  acc.z += __shfl_xor(acc.z, 32, 64);
-  acc.w += __shfl_xor(acc.w, 32, 64);
+  acc.x = xor_sum<32>(acc.x);
+  acc.y = xor_sum<32>(acc.y);
+  acc.z = xor_sum<32>(acc.z);
+  acc.w = xor_sum<32>(acc.w);
   if (lane < 32) red[wave][c4] = acc;
   __syncthreads();
   if (t < 32 && 4 * c4 < D) {
@@ -540,8 +540,8 @@ __global__ __launch_bounds__(256) void attn_prefill_f32(
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mb = fmaxf(mb, st[j][i]);
-      mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
-      mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+      mb = xor_max<16>(mb);
+      mb = xor_max<32>(mb);
       const float mn = fmaxf(m_run, mb * sl2);
       const bool none = mn == -INFINITY;  // no visible key yet: weights 0, alpha 1
       const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
@@ -580,8 +580,8 @@ __global__ __launch_bounds__(256) void attn_prefill_f32(
   }
 
   float l_tot = l_run;
-  l_tot += __shfl_xor(l_tot, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
+  l_tot = xor_sum<16>(l_tot);
+  l_tot = xor_sum<32>(l_tot);
   if (row_ok) {
     const float inv = 1.f / fmaxf(l_tot, eps);
     // out_tm: token-major [B, Lq, Hq, D] (the o_proj input); else [B, Hq, Lq, D]
@@ -795,7 +795,7 @@ void attn_prefill_mfma32(
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) mb = fmaxf(mb, sc[kb][i]);
-      mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+      mb = xor_max<32>(mb);
       // The reference maximum moves only when the tile's maximum exceeds it
       // by more than kRescaleSlack (log2 units): the exponentials stay below
       // 2^kRescaleSlack (exact in fp32, bf16's relative precision when
@@ -869,7 +869,7 @@ void attn_prefill_mfma32(
     }
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_tot = xor_sum<32>(l_run);
   if (row_ok) {
     const float inv = 1.f / fmaxf(l_tot, eps);
     // out_tm: token-major [B, Lq, Hq, D] (the o_proj input); else [B, Hq, Lq, D]

@@ -105,11 +105,42 @@ template <> struct Elem<bf16_t> {
 // ---------------------------------------------------------------- wave helpers
 // Cross-lane sums on DPP (no LDS round trip): within quads by quad_perm, then
 // 8- and 16-lane rows by row_half_mirror / row_mirror; wider groups finish
-// with xor shuffles.  After dpp_sum<W> every lane holds the sum of its
+// with lane swaps (xor_sum).  After dpp_sum<W> every lane holds the sum of its
 // aligned group of W lanes.
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// v combined with the value of the lane OFF (16 or 32) lanes away, as
+// v_permlane16_swap / v_permlane32_swap of v with itself: every lane ends up
+// with its own value in one result and its partner's in the other (which one
+// depends on the lane; sums and maxima do not care, and a + b == b + a
+// exactly).  Two VALU instructions instead of an LDS-routed ds_bpermute.
+// All 64 lanes must be active.
+template <int OFF>
+__device__ __forceinline__ float xor_sum(float v) {
+  static_assert(OFF == 16 || OFF == 32, "lane distance");
+  const uint32_t u = __float_as_uint(v);
+  if constexpr (OFF == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+template <int OFF>
+__device__ __forceinline__ float xor_max(float v) {
+  static_assert(OFF == 16 || OFF == 32, "lane distance");
+  const uint32_t u = __float_as_uint(v);
+  if constexpr (OFF == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
 }
 
 template <int W>
@@ -119,8 +150,8 @@ __device__ __forceinline__ float dpp_sum(float v) {
   if constexpr (W >= 4) v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
   if constexpr (W >= 8) v += dpp_f<0x141>(v);   // row_half_mirror
   if constexpr (W >= 16) v += dpp_f<0x140>(v);  // row_mirror
-  if constexpr (W >= 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (W >= 64) v += __shfl_xor(v, 32, 64);
+  if constexpr (W >= 32) v = xor_sum<16>(v);
+  if constexpr (W >= 64) v = xor_sum<32>(v);
   return v;
 }
 
@@ -132,8 +163,8 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<0x4E>(v));
   v = fmaxf(v, dpp_f<0x141>(v));
   v = fmaxf(v, dpp_f<0x140>(v));
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  v = xor_max<16>(v);
+  return xor_max<32>(v);
 }
 
 template <int W>
