@@ -194,7 +194,10 @@ def profile_prefill(iters=3):
 
 
 def attention_decode():
-    """Config 3: Hq32/Hkv8, D128, bf16 KV; append one token, then attend."""
+    """Config 3: Hq32/Hkv8, D128, bf16 KV.  Times the attend step over a cache
+    that already holds the appended token (L + 1 keys); the append itself is
+    one O(1) row write per layer and head (`strata_kv_append`), not timed
+    here."""
     import torch
     from lokahi_amd import ops
     dev = torch.device("cuda", 0)
