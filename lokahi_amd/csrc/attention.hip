@@ -13,6 +13,10 @@
 //     fill the GPU), keeps per-16-lane online-softmax state in registers,
 //     merges its lanes through LDS and writes (m, s, o[D]) partials;
 //     attn_decode_merge combines the chunks.
+//   * attn_decode_mfma : Lq == 1, bf16 q/k/v, batched heads (B * Hkv >= 64).
+//     One wave per (b, KV head, key chunk); the G query heads are the columns
+//     of 32x32x16 MFMAs, K/V tiles stream through a wave-private LDS ring;
+//     partials merged by attn_decode_merge.
 //   * attn_prefill_mfma32 : Lq > 1, bf16 q/k/v, D in {64, 128}.  Flash-style
 //     on 32x32x16 MFMA: 32-key K and V tiles streamed straight from global
 //     memory into LDS (two stages), S^T = K Q^T and O^T += V^T P^T, every
@@ -887,6 +891,240 @@ void attn_prefill_mfma32(
   }
 }
 
+// ---------------------------------------------------- batched decode on MFMA
+// One wave per (b, KV head, key chunk).  The G query heads of the KV head are
+// the columns of S^T = K Q^T on 32x32x16 MFMAs (columns past G hold zero q and
+// are ignored), so the online softmax is in-lane per head exactly as in the
+// prefill kernel; O^T += V^T P^T takes P^T straight from the S^T accumulator
+// and V^T through the LDS transpose read.  K and V tiles of 32 keys stream
+// through a ring of NST stages private to the wave (direct global -> LDS
+// loads, no barrier).  Partials (m, s, o[D]) per head go to `part` for
+// attn_decode_merge, or the output is finalised when there is one chunk.
+template <int D, int NST, int WPG>
+__global__ __launch_bounds__(64 * WPG) void attn_decode_mfma(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int B, int Hq, int Hkv,
+    int Lk, const int* __restrict__ dlen, int causal, int chunk, int nsplit, float scale,
+    float eps, float* __restrict__ part, bf16_t* __restrict__ out) {
+  constexpr int KT = 32;
+  constexpr int ROW = D * 2;
+  constexpr int NCHK = D / 8;
+  constexpr int TILE = KT * ROW;
+  constexpr int STAGE = 2 * TILE;
+  constexpr int AHEAD = NST - 1;
+  constexpr int NI = KT * NCHK / 64;   // 16-byte loads per lane per tile and operand
+  constexpr int QS = D / 16;
+  constexpr int DB = D / 32;
+  static_assert(NST == 2 || NST == 3, "two or three stages");
+  __shared__ __attribute__((aligned(16))) uint8_t lds_all[WPG * NST * STAGE];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int item = blockIdx.x * WPG + wave;
+  if (item >= B * Hkv * nsplit) return;  // wave-uniform; the kernel has no barrier
+  const int split = item % nsplit, bh = item / nsplit;
+  const int hkv = bh % Hkv, b = bh / Hkv;
+  const int G = Hq / Hkv;
+  const int c32 = lane & 31, h = lane >> 5;
+  const bool head_ok = c32 < G;
+  const int hq = hkv * G + (head_ok ? c32 : 0);
+  const int t0 = split * chunk;
+  const int tcap = min(Lk, t0 + chunk);  // keys in memory (the capacity in graph mode)
+  const bf16_t* kb = k + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  const bf16_t* vb = v + (int64_t)b * kv_bs + (int64_t)hkv * kv_hs;
+  const v4i32_t rk = rsrc(kb, (uint32_t)max(tcap, 0) * ROW);
+  const v4i32_t rv = rsrc(vb, (uint32_t)max(tcap, 0) * ROW);
+  uint8_t* lds = lds_all + wave * NST * STAGE;
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) uint8_t*)lds);
+  auto fk = [](int key) { return (key / (256 / ROW)) & (NCHK - 1); };
+  auto fv = [](int key) { return (key * (NCHK / 4)) & (NCHK - 1); };
+  uint32_t kvo[NI], vvo[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int slot = i * 64 + lane;
+    const int key = slot / NCHK, cp = slot % NCHK;
+    kvo[i] = key * ROW + 16 * (cp ^ fk(key));
+    vvo[i] = key * ROW + 16 * (cp ^ fv(key));
+  }
+  auto issue = [&](int kb0, int st) {
+    const uint32_t base = lds0 + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      dma16(base + i * 1024, kvo[i], rk, (uint32_t)kb0 * ROW);
+      dma16(base + TILE + i * 1024, vvo[i], rv, (uint32_t)kb0 * ROW);
+    }
+  };
+  const int nt = tcap > t0 ? (tcap - t0 + KT - 1) / KT : 0;
+  for (int t = 0; t < AHEAD && t < nt; ++t) issue(t0 + t * KT, t);
+  // Q^T fragments: column = this lane's head, k = head dims 16 s + 8 h .. +8
+  bf16x8_t qf[QS];
+  {
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(q) + ((int64_t)b * Hq + hq) * D;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      uint4 u = *reinterpret_cast<const uint4*>(qrow + s * 16 + 8 * h);
+      if (!head_ok) u = make_uint4(0, 0, 0, 0);
+      qf[s] = __builtin_bit_cast(bf16x8_t, u);
+    }
+  }
+  // Visible keys: [0, kend), read after the first tiles' loads are issued.
+  int cnt = Lk;
+  if (dlen) cnt = *dlen;
+  int kend = cnt;
+  if (causal) {
+    const int p = qpos ? qpos[b] : cnt - 1;
+    kend = min(cnt, p + 1);
+  }
+  const int t1 = min(kend, t0 + chunk);
+  int k_off[QS];
+#pragma unroll
+  for (int s = 0; s < QS; ++s) k_off[s] = c32 * ROW + 16 * ((2 * s + h) ^ fk(c32));
+  const int lp = lane & 15, gq = lane >> 4;
+  const int v_key = 4 * h + (lp >> 2);
+  const int v_col = 16 * (gq & 1) + 4 * (lp & 3);
+  int v_off[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    const int col = 32 * db + v_col;
+    v_off[db] = TILE + v_key * ROW + 16 * ((col / 8) ^ fv(v_key)) + 2 * (col % 8);
+  }
+  f32x16_t acc[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const float sl2 = scale * kLog2e;
+  auto wait_tiles = [&](int n) {
+    if (n <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if (n == 1) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * NI) : "memory");
+    else asm volatile("s_waitcnt vmcnt(%0)" :: "n"(4 * NI) : "memory");
+  };
+  // tiles past the visible keys are loaded (issued before the count was
+  // known) but not computed
+  const int ntv = t1 > t0 ? (t1 - t0 + KT - 1) / KT : 0;
+  auto tile = [&](int t, auto STC) {
+    constexpr int ST = decltype(STC)::value;
+    const int kb0 = t0 + t * KT;
+    if (t + AHEAD < nt) issue(kb0 + AHEAD * KT, (ST + AHEAD) % NST);
+    wait_tiles(min(nt - 1, t + AHEAD) - t);
+    const uint8_t* ks = lds + ST * STAGE;
+    if (kb0 + KT > t1) {
+      // V rows of keys past the visible ones may hold any bits (unwritten
+      // cache slots): zero them, so that p = 0 times them stays 0.
+      uint8_t* vt = lds + ST * STAGE + TILE;
+      const int r0 = max(t1 - kb0, 0);
+      for (int c = lane; c < (KT - r0) * NCHK; c += 64)
+        *reinterpret_cast<uint4*>(vt + r0 * ROW + 16 * c) = make_uint4(0, 0, 0, 0);
+    }
+    __builtin_amdgcn_s_setprio(1);
+    f32x16_t sc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      const uint4 a = *reinterpret_cast<const uint4*>(ks + k_off[s]);
+      sc = mfma32_bf16(__builtin_bit_cast(bf16x8_t, a), qf[s], sc);
+    }
+    __builtin_amdgcn_s_setprio(0);
+    if (kb0 + KT > t1) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kb0 + 8 * (i / 4) + 4 * h + i % 4;
+        sc[i] = key < t1 ? sc[i] : -INFINITY;
+      }
+    }
+    float mb = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mb = fmaxf(mb, sc[i]);
+    mb = xor_max<32>(mb);
+    const float mt = mb * sl2;
+    const float mn = mt > m_run + kRescaleSlack ? mt : m_run;
+    const bool none = mn == -INFINITY;
+    const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
+    const float nmn = none ? 0.f : -mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(sc[i], sl2, nmn));
+      sc[i] = p;
+      ps += p;
+    }
+    l_run = fmaf(l_run, alpha, ps);
+    m_run = mn;
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int i = 0; i < DB; ++i) acc[i] *= alpha;
+    }
+    __builtin_amdgcn_s_setprio(1);
+    // P enters the MFMA as bf16 hi + lo parts (p - bf16(p) is exact in fp32),
+    // so P V keeps about 16 significant bits of each weight, close to the
+    // fp32 weights of attn_decode_kernel, at twice the P V MFMAs (the kernel
+    // is bound by the K/V stream, not by the matrix cores).
+#pragma unroll
+    for (int s4 = 0; s4 < KT / 16; ++s4) {
+      const int i0 = 8 * s4;
+      uint32_t ph[4], pl[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float p0 = sc[i0 + 2 * c], p1 = sc[i0 + 2 * c + 1];
+        ph[c] = pack_bf16x2(p0, p1);
+        pl[c] = pack_bf16x2(p0 - __uint_as_float(ph[c] << 16),
+                            p1 - __uint_as_float(ph[c] & 0xffff0000u));
+      }
+      const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, make_uint4(ph[0], ph[1], ph[2], ph[3]));
+      const bf16x8_t pbl = __builtin_bit_cast(bf16x8_t, make_uint4(pl[0], pl[1], pl[2], pl[3]));
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        v4i16_t vv[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          vv[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4i16_t*)(lds0 + ST * STAGE + v_off[db] +
+                                                             (16 * s4 + 8 * j) * ROW));
+        uint4 au;
+        au.x = (uint16_t)vv[0][0] | ((uint32_t)(uint16_t)vv[0][1] << 16);
+        au.y = (uint16_t)vv[0][2] | ((uint32_t)(uint16_t)vv[0][3] << 16);
+        au.z = (uint16_t)vv[1][0] | ((uint32_t)(uint16_t)vv[1][1] << 16);
+        au.w = (uint16_t)vv[1][2] | ((uint32_t)(uint16_t)vv[1][3] << 16);
+        acc[db] = mfma32_bf16(__builtin_bit_cast(bf16x8_t, au), pb, acc[db]);
+        acc[db] = mfma32_bf16(__builtin_bit_cast(bf16x8_t, au), pbl, acc[db]);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+  for (int t = 0; t < ntv; t += NST) {
+    tile(t, std::integral_constant<int, 0>{});
+    if (t + 1 < ntv) tile(t + 1, std::integral_constant<int, 1>{});
+    if constexpr (NST == 3)
+      if (t + 2 < ntv) tile(t + 2, std::integral_constant<int, 2 % NST>{});
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the wave
+  const float l_tot = xor_sum<32>(l_run);
+  if (!head_ok) return;
+  // O^T accumulator: lane (c32, h) holds head c32, dims 32 db + 8 (i / 4) + 4 h + i % 4
+  if (nsplit == 1) {
+    const float inv = 1.f / fmaxf(l_tot, eps);
+    bf16_t* orow = out + ((int64_t)b * Hq + hq) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        Elem<bf16_t>::store(orow, 32 * db + 8 * (i / 4) + 4 * h + i % 4, acc[db][i] * inv);
+  } else {
+    float* pp = part + ((int64_t)b * Hq + hq) * part_stride(nsplit, D);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; i += 4)
+        *reinterpret_cast<float4*>(pp + split * D + 32 * db + 8 * (i / 4) + 4 * h) =
+            make_float4(acc[db][i], acc[db][i + 1], acc[db][i + 2], acc[db][i + 3]);
+    if (h == 0)
+      *reinterpret_cast<float2*>(pp + nsplit * D + 2 * split) =
+          make_float2(l_tot > 0.f ? m_run : -INFINITY, l_tot);
+  }
+}
+
 // ------------------------------------------------------------------ generic
 // One wave per (b, hq, query row); any D <= 256, any dtype mix.  Pass 1 finds
 // the row max and sum with lanes over keys; pass 2 has lanes over head dims.
@@ -978,11 +1216,60 @@ void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_ou
   *chunk_out = chunk;
 }
 
+// Batched heads (B * Hkv >= 64) with bf16 q/K/V run attn_decode_mfma: one
+// wave per (b, KV head, key chunk), about 4 waves per CU in all, chunks a
+// multiple of the 32-key tile and at least 64 keys.
+constexpr int kMfmaDecodeMinHeads = 64;
+constexpr int kMfmaDecodeWaves = 4;  // waves per workgroup (each with its own LDS ring)
+void decode_mfma_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
+  int ns = (num_cus * 4 + B * Hkv - 1) / (B * Hkv);
+  ns = std::max(1, std::min(ns, std::min(kMaxDecodeSplits, (Lcap + 63) / 64)));
+  int chunk = (Lcap + ns - 1) / ns;
+  chunk = std::max(32, (chunk + 31) / 32 * 32);
+  *nsplit_out = std::max(1, (Lcap + chunk - 1) / chunk);
+  *chunk_out = chunk;
+}
+
 template <typename TQ, typename TK, typename TV, int D>
 int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, int64_t kv_bs,
                   int64_t kv_hs, const int32_t* qpos, int B, int Hq, int Hkv, int Lk, int causal,
                   float scale, float eps, void* out, const AttnExtra& ex, hipStream_t stream) {
   const int G = Hq / Hkv;
+  if constexpr (sizeof(TQ) == 2 && sizeof(TK) == 2 && sizeof(TV) == 2) {
+    static const bool vector_only = getenv("STRATA_ATTN_DECODE_VECTOR") != nullptr;
+    if (B * Hkv >= kMfmaDecodeMinHeads && G <= 32 && !vector_only) {
+      // (B16 Hq32/Hkv8 D128 on MI355X: 1k keys 21.1 -> 16.5 us, 8k 106-110 ->
+      // 95.5 us, 32k 371-383 -> 355-369 us against attn_decode_kernel)
+      constexpr int WPG = kMfmaDecodeWaves;
+      int ns, ch;
+      decode_mfma_geometry(ctx->num_cus, B, Hkv, Lk, &ns, &ch);
+      float* pt = nullptr;
+      if (ns > 1) {
+        if (ex.part) {
+          if (ex.part_splits < ns)
+            return strata_set_error(STRATA_EINVAL, "decode attention: partials buffer too small");
+          pt = ex.part;
+        } else {
+          void* p = nullptr;
+          const int rc = strata_ctx_scratch(ctx, (size_t)B * Hq * part_stride(ns, D) * sizeof(float), &p, stream);
+          if (rc) return rc;
+          pt = reinterpret_cast<float*>(p);
+        }
+      }
+      const int items = B * Hkv * ns;
+      hipLaunchKernelGGL((attn_decode_mfma<D, 2, WPG>), dim3((items + WPG - 1) / WPG), dim3(64 * WPG),
+                         0, stream, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, kv_bs,
+                         kv_hs, qpos, B, Hq, Hkv, Lk, ex.dlen, causal, ch, ns, scale, eps, pt,
+                         (bf16_t*)out);
+      STRATA_HIP_CHECK(hipGetLastError());
+      if (ns > 1) {
+        hipLaunchKernelGGL((attn_decode_merge<TQ>), dim3(B * Hq), dim3(256), 0, stream, pt, ns, D,
+                           eps, (TQ*)out);
+        STRATA_HIP_CHECK(hipGetLastError());
+      }
+      return STRATA_OK;
+    }
+  }
   int nsplit, chunk;
   decode_split_geometry(ctx->num_cus, B, Hkv, Lk, &nsplit, &chunk);
   float* part = nullptr;
@@ -1100,6 +1387,11 @@ int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v,
 int strata_attn_decode_splits(strata_ctx* ctx, int B, int Hkv, int Lcap) {
   int nsplit, chunk;
   decode_split_geometry(ctx->num_cus, B, Hkv, Lcap, &nsplit, &chunk);
+  if (B * Hkv >= kMfmaDecodeMinHeads) {  // the MFMA kernel's count grows with Lcap
+    int n2;
+    decode_mfma_geometry(ctx->num_cus, B, Hkv, Lcap, &n2, &chunk);
+    nsplit = std::max(nsplit, n2);
+  }
   // The split count grows with the capacity within each regime of the
   // geometry (minimum chunk, splits per CU); the last capacity before a
   // regime boundary may need more splits than Lcap.

@@ -216,3 +216,24 @@ def test_decode_group_sizes_3_and_6(dev, Hq, dtype):
         tol = TOL_F32
     ref = att.chunked_gqa(q, k, v, None, True, 32768, 1024)
     assert rel_err(out, ref) < tol
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,L", [(16, 24, 8, 128, 300), (32, 8, 2, 64, 257),
+                                          (8, 64, 8, 128, 97)])
+def test_decode_batched_heads_mfma(dev, B, Hq, Hkv, D, L):
+    """B * Hkv >= 64 runs the MFMA decode kernel (the G query heads of a KV head
+    are the MFMA columns; G = 3, 4 and 8 here).  Per-row query positions cut
+    each row's visible keys at a different point, including inside a 32-key
+    tile and at the first key; the reference is float64 attention."""
+    from lokahi_amd import ops
+    rng = np.random.default_rng(B * 1000 + L)
+    q = round_bf16(rng.normal(size=(B, Hq, 1, D)).astype(np.float32))
+    k = round_bf16(rng.normal(size=(B, Hkv, L, D)).astype(np.float32))
+    v = round_bf16(rng.normal(size=(B, Hkv, L, D)).astype(np.float32))
+    pos = rng.integers(0, L, size=(B, 1))
+    pos[0, 0], pos[-1, 0] = 0, L - 1
+    out = to_np_f32(ops.attention(bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev),
+                                  query_positions=torch.from_numpy(pos.astype(np.int32))))
+    ref = att.naive_gqa(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64), pos)
+    assert rel_err(out, ref) < TOL_BF16
+    assert np.abs(out - ref).max() < 2e-2

@@ -162,3 +162,34 @@ def test_engine_long_context_across_split_regimes(dev):
     b = model.generate(prompt, max_new_tokens=400, use_graph=False).cpu()
     assert a.shape == (1, 6200)
     assert torch.equal(a, b)
+
+
+BATCH_HEADS = oll.Config(vocab_size=256, hidden_size=1024, intermediate_size=512,
+                         num_hidden_layers=2, num_attention_heads=16, num_key_value_heads=8,
+                         rms_norm_eps=1e-5, rope_theta=500000.0)
+
+
+def test_engine_batched_heads_decode_on_mfma(dev):
+    """8 rows x 8 KV heads reach the batched-heads threshold (64), so decode
+    attention runs one wave per (row, KV head, key chunk) on MFMA with
+    wave-private K/V rings.  Cache slots past the length hold NaN: the graph
+    steps (device-held key count, 256-key bucket capacity) fetch whole 32-key
+    tiles past the count, the host-launched steps do not.  Both must choose
+    the same tokens, and the op-by-op path (the same kernels driven from
+    Python) too.  The kernel itself is checked against float64 attention in
+    test_gpu_attention.py::test_decode_batched_heads_mfma; token parity with
+    the oracle is left to the smaller models above, whose top-2 logit margins
+    exceed the bf16 flow's logit error at every step."""
+    from lokahi_amd.llama import DecoderEngine
+    model, _ = _pair(BATCH_HEADS, seed=67, std=0.05)
+    prompt = torch.from_numpy(np.random.default_rng(67).integers(0, BATCH_HEADS.vocab_size, (8, 90)))
+    cache = model.new_cache(8, 320)
+    cache.k_storage.fill_(float("nan"))
+    cache.v_storage.fill_(float("nan"))
+    eng = DecoderEngine(model, cache, max_batch=8, max_tokens=8 * 90)
+    got = eng.generate(prompt, 8).cpu()
+    assert not torch.isnan(cache.k_storage[:, :, :, :97]).any()  # 90 prompt + 7 appended
+    host = model.generate(prompt, max_new_tokens=8, use_graph=False).cpu()
+    ops_path = model.generate(prompt, max_new_tokens=8, engine=False).cpu()
+    assert torch.equal(host, got)
+    assert torch.equal(ops_path, got)
