@@ -1216,10 +1216,21 @@ void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_ou
   *chunk_out = chunk;
 }
 
-// Batched heads (B * Hkv >= 64) with bf16 q/K/V run attn_decode_mfma: one
-// wave per (b, KV head, key chunk), about 4 waves per CU in all, chunks a
-// multiple of the 32-key tile and at least 64 keys.
+// bf16 decode over many (row, KV head, key) triples runs attn_decode_mfma:
+// batched heads (B * Hkv >= 64), or at least 64 Ki key-heads (batch 1 with 8
+// KV heads from 8k keys).  Below that the latency-bound vector kernel wins
+// (MI355X, Hq32/Hkv8 D128, MFMA against vector: B1/L2k 9.0 against 8.1 us,
+// B1/L8k 12.0 against 13.9, B1/L32k 27.1 against 30.5, B4/L8k 26.3 against
+// 30.7).  One wave per (b, KV head, key chunk), about 4 waves per CU in all,
+// chunks a multiple of the 32-key tile and at least 64 keys.
 constexpr int kMfmaDecodeMinHeads = 64;
+constexpr int64_t kMfmaDecodeMinKeyHeads = 65536;
+inline bool mfma_decode(int B, int Hkv, int64_t L) {
+  static const bool vector_only = getenv("STRATA_ATTN_DECODE_VECTOR") != nullptr;
+  static const bool mfma_always = getenv("STRATA_ATTN_DECODE_MFMA") != nullptr;
+  if (vector_only) return false;
+  return mfma_always || B * Hkv >= kMfmaDecodeMinHeads || (int64_t)B * Hkv * L >= kMfmaDecodeMinKeyHeads;
+}
 constexpr int kMfmaDecodeWaves = 4;  // waves per workgroup (each with its own LDS ring)
 void decode_mfma_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
   int ns = (num_cus * 4 + B * Hkv - 1) / (B * Hkv);
@@ -1236,10 +1247,10 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
                   float scale, float eps, void* out, const AttnExtra& ex, hipStream_t stream) {
   const int G = Hq / Hkv;
   if constexpr (sizeof(TQ) == 2 && sizeof(TK) == 2 && sizeof(TV) == 2) {
-    static const bool vector_only = getenv("STRATA_ATTN_DECODE_VECTOR") != nullptr;
-    if (B * Hkv >= kMfmaDecodeMinHeads && G <= 32 && !vector_only) {
-      // (B16 Hq32/Hkv8 D128 on MI355X: 1k keys 21.1 -> 16.5 us, 8k 106-110 ->
-      // 95.5 us, 32k 371-383 -> 355-369 us against attn_decode_kernel)
+    // (STRATA_ATTN_DECODE_VECTOR / STRATA_ATTN_DECODE_MFMA force either kernel)
+    if (G <= 32 && mfma_decode(B, Hkv, Lk)) {
+      // (B16 Hq32/Hkv8 D128 on MI355X against attn_decode_kernel: 1k keys
+      // 21.4 -> 17.3-18.0 us, 8k 113 -> 102 us, 32k 387 -> 370 us)
       constexpr int WPG = kMfmaDecodeWaves;
       int ns, ch;
       decode_mfma_geometry(ctx->num_cus, B, Hkv, Lk, &ns, &ch);
@@ -1387,7 +1398,7 @@ int dispatch_types(strata_ctx* ctx, const void* q, const void* k, const void* v,
 int strata_attn_decode_splits(strata_ctx* ctx, int B, int Hkv, int Lcap) {
   int nsplit, chunk;
   decode_split_geometry(ctx->num_cus, B, Hkv, Lcap, &nsplit, &chunk);
-  if (B * Hkv >= kMfmaDecodeMinHeads) {  // the MFMA kernel's count grows with Lcap
+  if (mfma_decode(B, Hkv, Lcap)) {  // the MFMA kernel's count grows with Lcap
     int n2;
     decode_mfma_geometry(ctx->num_cus, B, Hkv, Lcap, &n2, &chunk);
     nsplit = std::max(nsplit, n2);
