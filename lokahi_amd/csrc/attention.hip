@@ -1233,7 +1233,9 @@ inline bool mfma_decode(int B, int Hkv, int64_t L) {
 }
 constexpr int kMfmaDecodeWaves = 4;  // waves per workgroup (each with its own LDS ring)
 void decode_mfma_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
-  int ns = (num_cus * 4 + B * Hkv - 1) / (B * Hkv);
+  int per_cu = 4;
+  if (const char* e = getenv("STRATA_ATTN_MFMA_WAVES_PER_CU")) per_cu = std::max(1, atoi(e));
+  int ns = (num_cus * per_cu + B * Hkv - 1) / (B * Hkv);
   ns = std::max(1, std::min(ns, std::min(kMaxDecodeSplits, (Lcap + 63) / 64)));
   int chunk = (Lcap + ns - 1) / ns;
   chunk = std::max(32, (chunk + 31) / 32 * 32);
