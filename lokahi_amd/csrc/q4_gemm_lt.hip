@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <cstdlib>
 #include <map>
 #include <tuple>
@@ -202,7 +203,26 @@ int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const str
     }
     return STRATA_OK;
   }
+  // Rows the 256-row tiles do not cover run in slices of up to 64 rows on
+  // the skinny kernel (every weight read once per slice) when the shapes
+  // allow it: below 256 rows all of them, else the remainder.
   const int Mf = M / 256 * 256;
+  auto skinny_rows = [&](int m0, int rows, const strata_q4_weight* w, int n) -> int {
+    strata_q4_weight sl[kMaxGemmProblems];
+    for (int r0 = 0; r0 < rows; r0 += kSkinnyMaxRows) {
+      const int mr = std::min(kSkinnyMaxRows, rows - r0);
+      for (int i = 0; i < n; ++i) {
+        sl[i] = w[i];
+        sl[i].y = static_cast<char*>(w[i].y) + (size_t)(m0 + r0) * w[i].N * ye;
+      }
+      const int rc = strata_q4_gemm_skinny(static_cast<const uint16_t*>(x) + (size_t)(m0 + r0) * K,
+                                           mr, K, sl, n, y_dtype, stream);
+      if (rc) return rc;
+    }
+    return STRATA_OK;
+  };
+  const bool skinny = aligned16(x) && strata_q4_skinny_fits(1, K, ws, count);
+  if (skinny && Mf == 0) return skinny_rows(0, M, ws, count);
   strata_q4_weight big[kMaxGemmProblems];
   int nbig = 0;
   int64_t Nbig = 0;
@@ -229,6 +249,7 @@ int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const str
     rc = strata_q4_gemm_mfma_launch(x, Mf, K, big, nbig, y_dtype, scr, stream);
   }
   if (rc || Mf == M) return rc;
+  if (aligned16(x) && strata_q4_skinny_fits(1, K, big, nbig)) return skinny_rows(Mf, M - Mf, big, nbig);
   for (int i = 0; i < nbig; ++i) {
     rc = strata_q4_gemm_launch(static_cast<const uint16_t*>(x) + (size_t)Mf * K, M - Mf, K,
                                big[i].w, big[i].scales, big[i].biases, (int)big[i].N,

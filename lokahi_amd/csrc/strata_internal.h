@@ -65,6 +65,12 @@ int strata_q4_gemm_mfma_run(const void* x, int M, int K, const void* packed,
 // shapes allow, else one per linear.
 int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
                          int count, int y_dtype, void* stream, const void* packed = nullptr);
+// Linears sharing x for a few rows (M <= kSkinnyMaxRows, K % 512 == 0, every
+// N % 16 == 0, 16-byte aligned weights and x): one launch, each weight read once.
+constexpr int kSkinnyMaxRows = 64;
+bool strata_q4_skinny_fits(int M, int K, const strata_q4_weight* ws, int count);
+int strata_q4_gemm_skinny(const void* x, int M, int K, const strata_q4_weight* ws, int count,
+                          int y_dtype, void* stream);
 // bf16 [N, K] = s*q + b (fp32, one RNE rounding) of a q4 triple; K % 64 == 0,
 // w and out 16-byte aligned.
 int strata_q4_dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, int64_t N,
