@@ -226,11 +226,11 @@ void set_lengths(strata_decoder* d, int len) {
 // Load-time re-layout of the prefill weights (the MLX layout stays the
 // interchange and decode format): for each layer the four GEMM launches of a
 // prefill, in the layout of q4_gemm_relayout_kernel, when prefills can reach
-// the 256-row kernel and every linear qualifies.  Costs one more copy of the
+// the 256-column MFMA kernel and every linear qualifies.  Costs one more copy of the
 // q4 linears; on an allocation failure the prefill re-lays out per call.
 int pack_prefill_weights(strata_decoder* d) {
   const strata_llama_config& c = d->cfg;
-  if (d->max_tokens < kMfmaMinRows) return STRATA_OK;
+  if (d->max_tokens < kMfmaMidRows) return STRATA_OK;
   const int H = c.hidden_size, F = c.intermediate_size, QW = c.num_heads * c.head_dim;
   std::vector<void*> packed;
   for (const strata_llama_layer& L : d->layers) {

@@ -187,11 +187,9 @@ void strata_gemm_lt_destroy(strata_ctx* ctx) {
 
 int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
                          int count, int y_dtype, void* stream, const void* packed) {
-  // Default: the hand-written kernels only (fused dequant, bf16 MFMA):
-  // full 256-row tiles of every linear in one launch of the 256 x 256
-  // kernel, remaining rows (and linears whose N is not a multiple of 256)
-  // on the 128 x 128 kernel.  STRATA_GEMM_LT_MIN_M > 0 opts into the
-  // dequantize + hipBLASLt path from that many rows (comparison runs only).
+  // Default: the hand-written kernels only (fused dequant, bf16 MFMA).
+  // STRATA_GEMM_LT_MIN_M > 0 opts into the dequantize + hipBLASLt path from
+  // that many rows (comparison runs only).
   const char* e = getenv("STRATA_GEMM_LT_MIN_M");
   const int min_rows = e ? atoi(e) : 0;
   const size_t ye = y_dtype == STRATA_BF16 ? 2 : 4;
@@ -203,61 +201,70 @@ int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const str
     }
     return STRATA_OK;
   }
-  // Rows the 256-row tiles do not cover run in slices of up to 64 rows on
-  // the skinny kernel (every weight read once per slice) when the shapes
-  // allow it: below 256 rows all of them, else the remainder.
-  const int Mf = M / 256 * 256;
-  auto skinny_rows = [&](int m0, int rows, const strata_q4_weight* w, int n) -> int {
-    strata_q4_weight sl[kMaxGemmProblems];
-    for (int r0 = 0; r0 < rows; r0 += kSkinnyMaxRows) {
-      const int mr = std::min(kSkinnyMaxRows, rows - r0);
-      for (int i = 0; i < n; ++i) {
-        sl[i] = w[i];
-        sl[i].y = static_cast<char*>(w[i].y) + (size_t)(m0 + r0) * w[i].N * ye;
-      }
-      const int rc = strata_q4_gemm_skinny(static_cast<const uint16_t*>(x) + (size_t)(m0 + r0) * K,
-                                           mr, K, sl, n, y_dtype, stream);
-      if (rc) return rc;
-    }
-    return STRATA_OK;
-  };
-  const bool skinny = aligned16(x) && strata_q4_skinny_fits(1, K, ws, count);
-  if (skinny && Mf == 0) return skinny_rows(0, M, ws, count);
-  strata_q4_weight big[kMaxGemmProblems];
-  int nbig = 0;
-  int64_t Nbig = 0;
+  // Each linear goes its own way, so that it gives the same bits in a
+  // fused call as alone:
+  //   * from kMfmaMidRows rows, N a multiple of 256: the 256-column MFMA
+  //     kernel over all rows (a partial last row tile; K split over several
+  //     workgroups for linears with few tiles), the linears of one call in
+  //     as few launches as their splits allow;
+  //   * below that, shapes the skinny kernel takes (K % 512 == 0, N % 16 ==
+  //     0): the skinny kernel, rows in slices of 64, one launch per slice;
+  //   * anything else: the 128 x 128 kernel, one launch per linear.
+  int mid_min = kMfmaMidRows;
+  if (const char* em = getenv("STRATA_GEMM_MFMA_MIN_M")) mid_min = atoi(em);
+  const bool x_ok = aligned16(x) && K % 64 == 0 && (uint64_t)M * K * 2 < (1ull << 32);
+  strata_q4_weight fast[kMaxGemmProblems];
+  int nfast = 0;
+  int64_t Nfast = 0;
   for (int i = 0; i < count; ++i) {
-    const bool fits = Mf >= kMfmaMinRows && ws[i].N % 256 == 0 && aligned16(ws[i].w) &&
-                      nbig < kMaxGemmProblems;
-    if (fits) {
-      big[nbig++] = ws[i];
-      Nbig += ws[i].N;
+    bool f = false;
+    if (M >= mid_min)
+      f = x_ok && ws[i].N % 256 == 0 && aligned16(ws[i].w) &&
+          (uint64_t)(Nfast + ws[i].N) * K / 2 < (1ull << 32);
+    else
+      f = aligned16(x) && strata_q4_skinny_fits(1, K, &ws[i], 1);
+    if (f && nfast < kMaxGemmProblems) {
+      fast[nfast++] = ws[i];
+      Nfast += ws[i].N;
     } else {
       const int rc = strata_q4_gemm_launch(x, M, K, ws[i].w, ws[i].scales, ws[i].biases,
                                            (int)ws[i].N, ws[i].y, y_dtype, stream);
       if (rc) return rc;
     }
   }
-  if (nbig == 0) return STRATA_OK;
-  int rc;
-  if (packed && nbig == count) {  // weights re-laid out at load time, in this order
-    rc = strata_q4_gemm_mfma_run(x, Mf, K, packed, big, nbig, y_dtype, stream);
-  } else {
-    void* scr = nullptr;
-    rc = strata_ctx_scratch(ctx, strata_q4_gemm_mfma_scratch(Nbig, K), &scr, stream);
-    if (rc) return rc;
-    rc = strata_q4_gemm_mfma_launch(x, Mf, K, big, nbig, y_dtype, scr, stream);
+  if (nfast == 0) return STRATA_OK;
+  if (M < mid_min) {
+    for (int r0 = 0; r0 < M; r0 += kSkinnyMaxRows) {
+      const int mr = std::min(kSkinnyMaxRows, M - r0);
+      strata_q4_weight sl[kMaxGemmProblems];
+      for (int i = 0; i < nfast; ++i) {
+        sl[i] = fast[i];
+        sl[i].y = static_cast<char*>(fast[i].y) + (size_t)r0 * fast[i].N * ye;
+      }
+      const int rc = strata_q4_gemm_skinny(static_cast<const uint16_t*>(x) + (size_t)r0 * K, mr,
+                                           K, sl, nfast, y_dtype, stream);
+      if (rc) return rc;
+    }
+    return STRATA_OK;
   }
-  if (rc || Mf == M) return rc;
-  if (aligned16(x) && strata_q4_skinny_fits(1, K, big, nbig)) return skinny_rows(Mf, M - Mf, big, nbig);
-  for (int i = 0; i < nbig; ++i) {
-    rc = strata_q4_gemm_launch(static_cast<const uint16_t*>(x) + (size_t)Mf * K, M - Mf, K,
-                               big[i].w, big[i].scales, big[i].biases, (int)big[i].N,
-                               static_cast<char*>(big[i].y) + (size_t)Mf * big[i].N * ye, y_dtype,
-                               stream);
+  // The decoder's load-time re-layout covers all of the call's linears in
+  // order; otherwise this call re-lays the weights out into the scratch
+  // arena, ahead of the fp32 partial sums of split linears.
+  const void* pk_in = nfast == count ? packed : nullptr;
+  const size_t pb = strata_q4_gemm_mfma_part_bytes(M, K, fast, nfast);
+  const size_t pk = pk_in ? 0 : (strata_q4_gemm_mfma_scratch(Nfast, K) + 255) / 256 * 256;
+  void* scr = nullptr;
+  if (pk + pb > 0) {
+    const int rc = strata_ctx_scratch(ctx, pk + pb, &scr, stream);
     if (rc) return rc;
   }
-  return STRATA_OK;
+  if (!pk_in) {
+    const int rc = strata_q4_gemm_pack(fast, nfast, K, scr, stream);
+    if (rc) return rc;
+    pk_in = scr;
+  }
+  float* part = pb ? reinterpret_cast<float*>(static_cast<char*>(scr) + pk) : nullptr;
+  return strata_q4_gemm_mfma_run(x, M, K, pk_in, fast, nfast, y_dtype, stream, part, pb);
 }
 
 int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t* w,

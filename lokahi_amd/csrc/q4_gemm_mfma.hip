@@ -29,6 +29,8 @@
 //   * Workgroup order: tiles are dealt to the 8 XCDs in contiguous runs
 //     (block b runs on XCD b % 8), grouped 4 M-tiles x N-tiles, so the
 //     ~32 workgroups resident on one XCD share X and W tiles in its L2.
+#include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "strata_internal.h"
@@ -80,12 +82,9 @@ __device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float b) {
   return o;
 }
 
-// Tile index -> (m tile, n tile): XCD-contiguous runs, then groups of
-// kGroupM M tiles sweeping the N tiles.
-__device__ __forceinline__ void tile_of(int b, int mt, int nt, int* tm, int* tn) {
-  const int total = mt * nt;
-  int t = b;
-  if (total % 8 == 0) t = (b % 8) * (total / 8) + b / 8;
+// Tile index -> (m tile, n tile): groups of kGroupM M tiles sweeping the
+// N tiles.
+__device__ __forceinline__ void group_tile(int t, int mt, int nt, int* tm, int* tn) {
   const int per_group = kGroupM * nt;
   const int grp = t / per_group, rem = t - grp * per_group;
   const int gm = min(kGroupM, mt - grp * kGroupM);
@@ -101,8 +100,8 @@ constexpr int kWBytes = 4 * 64 * 32;             // 8 KB
 constexpr int kSBBytes = 4 * 64 * 4;             // 1 KB
 constexpr int kStages = 3;
 
-// Full tiles only: M % 256 == 0, N % 256 == 0, K % 64 == 0, and every
-// operand under 4 GiB (the launcher checks).
+// N % 256 == 0, K % 64 == 0, and every operand under 4 GiB (the launcher
+// checks); any M.
 // Per-M-tile constants: TM = 256 (one workgroup per CU) or 128 (two per
 // CU, for problems with few 256-row tiles).
 template <int TM>
@@ -124,11 +123,22 @@ struct GemmOut {
   int count;
 };
 
+// The part of the problem space one launch covers: M tiles 0 .. mt - 1 (the
+// last one may be partial: rows at or past M read as zero and are not
+// stored), N tiles ntile0 .. ntile0 + nts - 1 of the re-laid-out weight, and
+// S slices of the K groups.  With S > 1 each slice writes its fp32 partial
+// sums to part [S][mt * TM][nts * 256] and q4_gemm_splitk_reduce adds them
+// up in slice order.
+struct GemmSplit {
+  int mt, ntile0, nts, S;
+  float* part;
+};
+
 template <int TM, typename YT>
 __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(TM == 256 ? 1 : 2, TM == 256 ? 1 : 2)))
 void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
                          const uint32_t* __restrict__ wt, const uint32_t* __restrict__ sbt,
-                         int N, GemmOut out) {
+                         int N, GemmOut out, GemmSplit sp) {
   constexpr int MB = Tile<TM>::MB, XCH = Tile<TM>::XCH, kXBytes = Tile<TM>::kXBytes;
   constexpr int kStage = Tile<TM>::kStage, kDmaPerStep = Tile<TM>::kDmaPerStep;
   constexpr int QPS = 8 / MB;  // dequant quarters per sub-step
@@ -138,13 +148,19 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   constexpr int kReadSt = 3 * MB - 4;
   static_assert(kReadSt - 1 >= kDmaPerStep - 1, "the load wait must follow step g + 2's issue");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int mt = M / TM, nt = N / TN;
-  int tmi, tni;
-  tile_of(blockIdx.x, mt, nt, &tmi, &tni);
-  const int m0 = tmi * TM, n0 = tni * TN;
+  // Workgroups are dealt to the 8 XCDs in contiguous runs of the (slice,
+  // tile) order (block b runs on XCD b % 8), so a run shares its K slice.
+  const int mt = sp.mt, nts = sp.nts, S = sp.S, tiles = mt * nts;
+  int u = blockIdx.x;
+  if ((tiles * S) % 8 == 0) u = (u % 8) * (tiles * S / 8) + u / 8;
+  const int ks = u / tiles;
+  int tmi, tnl;
+  group_tile(u - ks * tiles, mt, nts, &tmi, &tnl);
+  const int m0 = tmi * TM, n0 = (sp.ntile0 + tnl) * TN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = K / TK;
+  const int g0 = (int)((int64_t)ks * G / S), g1 = (int)((int64_t)(ks + 1) * G / S);
   const uint32_t kb = (uint32_t)K * 2;   // bytes per X row
   const uint32_t wgb = (uint32_t)N * 32;  // bytes per group of the re-laid-out codes
   const uint32_t sgb = (uint32_t)N * 4;   // bytes per group of (s, b) words
@@ -259,8 +275,8 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 
   // prologue: steps 0 and 1 in flight; step 0 complete and its k block 0
   // dequantized (k blocks 1-3 follow during step 0).
-  issue(0, 0);
-  issue(min(1, G - 1), 1);
+  issue(g0, 0);
+  issue(min(g0 + 1, g1 - 1), 1);
   vm_wait_step();
   __syncthreads();
   read_sb(0, dsbn);
@@ -288,10 +304,10 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   // In the last step the loads repeat the last step's addresses and the
   // fragments dequantized for the step after it are never used.
   int stg = 0;
-  for (int g = 0; g < G; ++g) {
+  for (int g = g0; g < g1; ++g) {
     const int stg1 = stg == kStages - 1 ? 0 : stg + 1;
     const int stg2 = stg1 == kStages - 1 ? 0 : stg1 + 1;
-    const int gn = min(g + 2, G - 1);
+    const int gn = min(g + 2, g1 - 1);
     const uint8_t* xb = lds + stg * kStage;
     uint4 a = *reinterpret_cast<const uint4*>(xb + aoff(0, 0));
     uint4 an = *reinterpret_cast<const uint4*>(xb + aoff(1 % MB, 1 / MB));
@@ -337,8 +353,20 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 #endif
     stg = stg1;
   }
-  // C layout: lane holds column c32, rows 8 (i / 4) + 4 kh + i % 4.  The
-  // tile's problem (wave-uniform): the last one starting at or before n0.
+  // C layout: lane holds column c32, rows 8 (i / 4) + 4 kh + i % 4.
+  if (sp.part) {  // this K slice's fp32 partial sums, every row of the tile
+    const int ld = nts * TN;
+    float* pb = sp.part + ((int64_t)ks * (mt * TM) + m0 + 4 * kh) * ld + tnl * TN + wave * WN + c32;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          pb[(int64_t)(mb * 32 + 8 * (i / 4) + i % 4) * ld + nb * 32] = acc[mb][nb][i];
+    return;
+  }
+  // The tile's problem (wave-uniform): the last one starting at or before n0.
   int p = 0;
 #pragma unroll
   for (int t = 1; t < kMaxGemmProblems; ++t)
@@ -346,13 +374,44 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   const int np = out.n0[p + 1] - out.n0[p];
   YT* yb = static_cast<YT*>(out.y[p]) + (int64_t)(m0 + 4 * kh) * np + (n0 - out.n0[p]) +
            wave * WN + c32;
+  const int rows_left = M - (m0 + 4 * kh);  // rows of a partial last tile are not stored
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        Elem<YT>::store(yb, (int64_t)(mb * 32 + 8 * (i / 4) + i % 4) * np + nb * 32, acc[mb][nb][i]);
+      for (int i = 0; i < 16; ++i) {
+        const int r = mb * 32 + 8 * (i / 4) + i % 4;
+        if (r < rows_left) Elem<YT>::store(yb, (int64_t)r * np + nb * 32, acc[mb][nb][i]);
+      }
+}
+
+// y[m, c] = sum over slices s = 0 .. S - 1, in that order, of
+// part[s][m][col0 + c], for one linear's ncols columns (a multiple of 4)
+// inside partial rows ld columns wide; four columns per thread.
+template <typename YT>
+__global__ __launch_bounds__(256) void q4_gemm_splitk_reduce(const float* __restrict__ part, int S,
+                                                             int64_t slice, int ld, int col0, int M,
+                                                             int ncols, YT* __restrict__ y) {
+  const int c4 = ncols >> 2;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * c4) return;
+  const int64_t m = i / c4;
+  const int64_t c = (i - m * c4) * 4;
+  const float* pp = part + m * ld + col0 + c;
+  float4 a = *reinterpret_cast<const float4*>(pp);
+  for (int s = 1; s < S; ++s) {
+    const float4 b = *reinterpret_cast<const float4*>(pp + s * slice);
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+  }
+  const int64_t off = m * ncols + c;
+  Elem<YT>::store(y, off, a.x);
+  Elem<YT>::store(y, off + 1, a.y);
+  Elem<YT>::store(y, off + 2, a.z);
+  Elem<YT>::store(y, off + 3, a.w);
 }
 
 // Re-layout of one q4 weight for the kernel above (a pass over the weight,
@@ -435,6 +494,87 @@ int strata_q4_gemm_pack(const strata_q4_weight* ws, int count, int K, void* pack
   return STRATA_OK;
 }
 
+namespace {
+int num_cus() {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  return cus;
+}
+
+// K slices for one linear of N columns at M rows.  The 128-row tiles times
+// the slices aim at one workgroup per CU for long rows (K >= 8192) and half
+// that otherwise (measured on the 8B shapes at 128-512 rows: more slices
+// cost more in partial sums than they gain); a power of two, each slice at
+// least 4 K groups, at most 16 (8 below K = 8192, so that q, k and v
+// share a launch).  It depends on (M, K, N) only, so a linear
+// gives the same bits in a fused launch and alone.  STRATA_GEMM_SPLITK
+// overrides it (timing runs).
+int splitk_slices(int M, int K, int N, int cus) {
+  const int G = K / TK;
+  // A narrow linear (k, v) counts as 16 column tiles: it then gets the
+  // slices of the 4096-column one (q) it is usually launched with.
+  const int64_t tiles = (int64_t)((M + 127) / 128) * std::max(N / TN, 16);
+  const int64_t target = G >= 128 ? cus : cus / 2;
+  int S = tiles >= target ? 1 : (int)(target / tiles);
+  int p2 = 1;
+  while (p2 * 2 <= S) p2 *= 2;
+  S = p2;
+  if (const char* e = getenv("STRATA_GEMM_SPLITK")) S = atoi(e);
+  S = std::min(S, std::min(G >= 128 ? 16 : 8, std::max(1, G / 4)));
+  return std::max(S, 1);
+}
+
+size_t splitk_part_bytes(int M, int N, int S) {
+  return S > 1 ? (size_t)S * ((M + 127) / 128 * 128) * N * 4 : 0;
+}
+
+// Slices of each linear, and runs of consecutive linears with the same
+// slice count (one launch each): run r covers linears first[r] ..
+// first[r + 1] - 1.
+struct SplitPlan {
+  int S[kMaxGemmProblems];
+  int first[kMaxGemmProblems + 1];
+  int runs;
+};
+SplitPlan split_plan(int M, int K, const strata_q4_weight* ws, int count, int cus, bool allow) {
+  SplitPlan pl{};
+  for (int p = 0; p < count; ++p) pl.S[p] = allow ? splitk_slices(M, K, (int)ws[p].N, cus) : 1;
+  pl.runs = 0;
+  for (int p = 0; p < count; ++p)
+    if (p == 0 || pl.S[p] != pl.S[p - 1]) pl.first[pl.runs++] = p;
+  pl.first[pl.runs] = count;
+  return pl;
+}
+size_t plan_part_bytes(const SplitPlan& pl, int M, const strata_q4_weight* ws) {
+  size_t need = 0;
+  for (int r = 0; r < pl.runs; ++r) {
+    int64_t n = 0;
+    for (int p = pl.first[r]; p < pl.first[r + 1]; ++p) n += ws[p].N;
+    need = std::max(need, splitk_part_bytes(M, (int)n, pl.S[pl.first[r]]));
+  }
+  return need;
+}
+
+template <int TM, typename YT>
+void gemm_go(const void* x, int M, int K, const uint32_t* wt, const uint32_t* sbt, int N,
+             const GemmOut& out, const GemmSplit& sp, hipStream_t st) {
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void*)q4_gemm_mfma_kernel<TM, YT>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, Tile<TM>::kLds);
+    attr = true;
+  }
+  hipLaunchKernelGGL((q4_gemm_mfma_kernel<TM, YT>), dim3(sp.mt * sp.nts * sp.S), dim3(NTHR),
+                     Tile<TM>::kLds, st, (const uint16_t*)x, M, K, wt, sbt, N, out, sp);
+}
+}  // namespace
+
+size_t strata_q4_gemm_mfma_part_bytes(int M, int K, const strata_q4_weight* ws, int count) {
+  if (count < 1 || count > kMaxGemmProblems) return 0;
+  return plan_part_bytes(split_plan(M, K, ws, count, num_cus(), true), M, ws);
+}
+
 int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const strata_q4_weight* ws, int count,
                                int y_dtype, void* scratch, void* stream) {
   const int rc = strata_q4_gemm_pack(ws, count, K, scratch, stream);
@@ -443,43 +583,60 @@ int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const strata_q4_weig
 }
 
 int strata_q4_gemm_mfma_run(const void* x, int M, int K, const void* packed,
-                            const strata_q4_weight* ws, int count, int y_dtype, void* stream) {
+                            const strata_q4_weight* ws, int count, int y_dtype, void* stream,
+                            float* part, size_t part_bytes) {
   STRATA_REQUIRE(K % TK == 0 && K >= TK, "q4 GEMM: K must be a positive multiple of 64");
   GemmOut out;
   int N = 0;
   int rc = gemm_problems(ws, count, &out, &N);
   if (rc) return rc;
-  STRATA_REQUIRE(M % 256 == 0 && M > 0, "q4 GEMM (256-tile kernel): M must be a positive multiple of 256");
+  STRATA_REQUIRE(M > 0, "q4 GEMM (256-column kernel): M must be positive");
   STRATA_REQUIRE((uint64_t)M * K * 2 < (1ull << 32) && (uint64_t)N * K / 2 < (1ull << 32),
-                 "q4 GEMM (256-tile kernel): operands must be under 4 GiB");
+                 "q4 GEMM (256-column kernel): operands must be under 4 GiB");
   STRATA_REQUIRE(packed && (reinterpret_cast<uintptr_t>(packed) & 15) == 0,
                  "q4 GEMM: unaligned packed buffer");
   const uint32_t* wt = static_cast<const uint32_t*>(packed);
   const uint32_t* sbt = wt + (size_t)N * K / 8;
-  // 256-row tiles unless that leaves the GPU under two workgroups per CU.
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess)
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  const bool big = (int64_t)(M / 256) * (N / TN) >= 2 * cus;
-#define STRATA_GEMM_GO(TMV, YT)                                                                   \
-  {                                                                                               \
-    static bool attr = false;                                                                     \
-    if (!attr) {                                                                                  \
-      STRATA_HIP_CHECK(hipFuncSetAttribute((const void*)q4_gemm_mfma_kernel<TMV, YT>,             \
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,            \
-                                           Tile<TMV>::kLds));                                     \
-      attr = true;                                                                                \
-    }                                                                                             \
-    hipLaunchKernelGGL((q4_gemm_mfma_kernel<TMV, YT>), dim3((M / TMV) * (N / TN)), dim3(NTHR),    \
-                       Tile<TMV>::kLds, as_stream(stream), (const uint16_t*)x, M, K, wt, sbt, N,  \
-                       out);                                                                      \
+  hipStream_t st = as_stream(stream);
+  const bool bf = y_dtype == STRATA_BF16;
+  const int cus = num_cus();
+  // A launch over columns [ntile0, ntile0 + nts) tiles with S slices: 256-row
+  // tiles unless that leaves the GPU under two workgroups per CU.
+  auto go = [&](int ntile0, int nts, int S) {
+    const bool big = S == 1 && (int64_t)((M + 255) / 256) * nts >= 2 * cus;
+    const int TM = big ? 256 : 128;
+    const GemmSplit sp{(M + TM - 1) / TM, ntile0, nts, S, S > 1 ? part : nullptr};
+    if (big) {
+      if (bf) gemm_go<256, bf16_t>(x, M, K, wt, sbt, N, out, sp, st);
+      else gemm_go<256, float>(x, M, K, wt, sbt, N, out, sp, st);
+    } else {
+      if (bf) gemm_go<128, bf16_t>(x, M, K, wt, sbt, N, out, sp, st);
+      else gemm_go<128, float>(x, M, K, wt, sbt, N, out, sp, st);
+    }
+  };
+  SplitPlan pl = split_plan(M, K, ws, count, cus, part != nullptr);
+  if (plan_part_bytes(pl, M, ws) > part_bytes) pl = split_plan(M, K, ws, count, cus, false);
+  // One launch per run of linears with the same slice count; a split run is
+  // followed by the in-order sum of its slices per linear (the partial
+  // buffer is reused run after run, in stream order).
+  for (int r = 0; r < pl.runs; ++r) {
+    const int pa = pl.first[r], pe = pl.first[r + 1], S = pl.S[pa];
+    const int c0 = out.n0[pa], ncols = out.n0[pe] - c0;
+    go(c0 / TN, ncols / TN, S);
+    if (S == 1) continue;
+    STRATA_HIP_CHECK(hipGetLastError());
+    const int64_t slice = (int64_t)((M + 127) / 128 * 128) * ncols;
+    for (int p = pa; p < pe; ++p) {
+      const int np = (int)ws[p].N;
+      const unsigned blocks = (unsigned)(((int64_t)M * (np / 4) + 255) / 256);
+      if (bf)
+        hipLaunchKernelGGL(q4_gemm_splitk_reduce<bf16_t>, dim3(blocks), dim3(256), 0, st, part, S,
+                           slice, ncols, out.n0[p] - c0, M, np, static_cast<bf16_t*>(ws[p].y));
+      else
+        hipLaunchKernelGGL(q4_gemm_splitk_reduce<float>, dim3(blocks), dim3(256), 0, st, part, S,
+                           slice, ncols, out.n0[p] - c0, M, np, static_cast<float*>(ws[p].y));
+    }
   }
-  if (y_dtype == STRATA_BF16) {
-    if (big) STRATA_GEMM_GO(256, bf16_t) else STRATA_GEMM_GO(128, bf16_t)
-  } else {
-    if (big) STRATA_GEMM_GO(256, float) else STRATA_GEMM_GO(128, float)
-  }
-#undef STRATA_GEMM_GO
   STRATA_HIP_CHECK(hipGetLastError());
   return STRATA_OK;
 }

@@ -44,13 +44,13 @@ int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t*
                    const uint16_t* s, const uint16_t* b, int N, void* y, int y_dtype,
                    void* stream);
 void strata_gemm_lt_destroy(strata_ctx* ctx);
-// 256 x 256-tile fused-dequant MFMA GEMM (M >= kMfmaMinRows on the default path).
-constexpr int kMfmaMinRows = 256;
+// 256-column-tile fused-dequant MFMA GEMM (M >= kMfmaMidRows on the default
+// path).
 // scratch: strata_q4_gemm_mfma_scratch(N, K) bytes, 16-byte aligned (the
 // weight's per-call re-layout).
 size_t strata_q4_gemm_mfma_scratch(int64_t N, int K);
 // The linears of `ws` (same x; N of each a multiple of 256) in one launch of
-// the 256-column-tile kernel, full 256-row tiles only (M % 256 == 0).
+// the 256-column-tile kernel, without a K split.
 constexpr int kMaxGemmProblems = 8;
 int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const strata_q4_weight* ws, int count,
                                int y_dtype, void* scratch, void* stream);
@@ -59,8 +59,18 @@ int strata_q4_gemm_mfma_launch(const void* x, int M, int K, const strata_q4_weig
 // once at load time by the decoder), then GEMMs on it (the ws' w, scales and
 // biases are not read, only N and y).
 int strata_q4_gemm_pack(const strata_q4_weight* ws, int count, int K, void* packed, void* stream);
+// Any M.  With `part` (fp32 scratch of part_bytes), linears whose tiles
+// leave CUs idle split K over several workgroups and add the slices up in
+// order (strata_q4_gemm_mfma_part_bytes sizes it); without it, no split.
 int strata_q4_gemm_mfma_run(const void* x, int M, int K, const void* packed,
-                            const strata_q4_weight* ws, int count, int y_dtype, void* stream);
+                            const strata_q4_weight* ws, int count, int y_dtype, void* stream,
+                            float* part = nullptr, size_t part_bytes = 0);
+size_t strata_q4_gemm_mfma_part_bytes(int M, int K, const strata_q4_weight* ws, int count);
+// From this many rows the linears sharing x go to the 256-column MFMA kernel
+// when every N is a multiple of 256 (STRATA_GEMM_MFMA_MIN_M overrides).
+// (Measured on the 8B shapes: the skinny kernel is faster up to ~32 rows,
+// this one from ~48.)
+constexpr int kMfmaMidRows = 40;
 // Prefill linears sharing x (M > 8 rows, bf16 x): one launch where the
 // shapes allow, else one per linear.
 int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,

@@ -86,9 +86,9 @@ def test_config5_layer_gemms_8k_sampled_rows(dev, name, N, K):
 
 
 def test_multi_linear_gemm_one_launch_equals_separate_launches(dev):
-    """q/k/v-shaped linears in one launch of the 256-tile kernel (weights
+    """q/k/v-shaped linears in one launch of the 256-column kernel (weights
     re-laid side by side, each tile writing its own output) against one
-    launch per linear; M = 8192 + 100 covers the remainder rows, and a
+    launch per linear; M = 8192 + 100 ends in a partial row tile, and a
     linear whose N is not a multiple of 256 takes the 128-tile kernel."""
     from lokahi_amd import ops
     M, K = 8192 + 100, 4096

@@ -178,11 +178,12 @@ def test_gemm_library_plan_cache_survives_many_prompt_lengths(dev, monkeypatch):
 @pytest.mark.parametrize("M,K", [(9, 1024), (16, 3584), (17, 1024), (40, 2048), (64, 1024),
                                  (65, 1024), (150, 512), (300, 1024)])
 def test_gemm_few_rows_skinny_kernel(dev, M, K):
-    """9-64 rows (and the rows past the last 256-row tile) run the skinny
-    kernel: 16 or 64 output columns per workgroup, the K quarters of each
-    column block summed in LDS, rows in slices of 64.  q/k/v-like linears in
-    one launch, bf16 and fp32 outputs, against x @ bf16(dequant(W)).T in
-    float64, and bit-identical to separate launches of each linear."""
+    """Up to 39 rows the skinny kernel runs: 16 or 64 output columns per
+    workgroup, the K quarters of each column block summed in LDS (from 40
+    rows, linears whose N is a multiple of 256 take the MFMA kernel, whose
+    own test follows).  q/k/v-like linears in one launch, bf16 and fp32
+    outputs, against x @ bf16(dequant(W)).T in float64, and bit-identical to
+    separate launches of each linear."""
     from lokahi_amd import ops
     rng = np.random.default_rng(M * 7 + K)
     ns = (1024, 256, 256) if M != 16 else (16384, 16, 48)  # 64- and 16-column blocks
@@ -199,3 +200,32 @@ def test_gemm_few_rows_skinny_kernel(dev, M, K):
         assert rel_err(to_np_f32(a16), q4.quantized_matmul(bf16_bits_to_f32(x), w, s, b)) < TOL_BF16
         alone = ops.linear(xd, *dp, out_dtype=torch.float32)
         assert torch.equal(alone, a32)
+
+
+@pytest.mark.parametrize("M,K,ns", [(65, 4096, (4096, 1024, 1024)), (100, 1024, (1024, 256, 256)),
+                                    (128, 4096, (14336,)), (200, 14336, (4096,)),
+                                    (255, 2048, (512, 1536)), (300, 1024, (1024, 256, 256)),
+                                    (777, 4096, (4096,))])
+def test_gemm_mid_rows_split_k(dev, M, K, ns):
+    """40 rows and up, N a multiple of 256: the 256-column MFMA
+    kernel over all rows (a partial last row tile), each linear whose tiles
+    leave CUs idle split over K slices whose fp32 partial sums are added in
+    slice order.  Against x @ bf16(dequant(W)).T in float64 and the oracle's
+    q4 matmul; a linear gives the same bits in a fused launch as alone (the
+    split depends on its own M, K and N only)."""
+    from lokahi_amd import ops
+    rng = np.random.default_rng(M * 11 + K)
+    probs = [_problem(rng, n, K)[:3] for n in ns]
+    x = f32_to_bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
+    dprobs = [tuple(to_dev(a, dev) for a in p) for p in probs]
+    xd = to_dev(x, dev)
+    y32 = ops.linear_multi(xd, dprobs, out_dtype=torch.float32)
+    y16 = ops.linear_multi(xd, dprobs)
+    xf = bf16_bits_to_f32(x)
+    for (w, s, b), a32, a16, dp in zip(probs, y32, y16, dprobs):
+        wq = round_bf16(q4.dequantize(w, s, b, 64).astype(np.float32)).astype(np.float64)
+        ref_b = xf.astype(np.float64) @ wq.T
+        assert rel_err(to_np_f32(a32), ref_b) < TOL_F32
+        assert rel_err(to_np_f32(a16), q4.quantized_matmul(xf, w, s, b)) < TOL_BF16
+        assert torch.equal(ops.linear(xd, *dp, out_dtype=torch.float32), a32)
+        assert torch.equal(ops.linear(xd, *dp), a16)
