@@ -12,6 +12,8 @@
 // The KV append replaces MLXKVCache.update's concatenate
 // (src/ollm/mlx_kvcache.py:65-125) with an O(Lnew) write into a
 // preallocated [B, Hkv, Lmax, D] buffer per layer.
+#include <algorithm>
+
 #include "strata_common.h"
 
 namespace {
@@ -55,7 +57,9 @@ __global__ void kv_copy(const TS* __restrict__ src, TC* __restrict__ dst, int B,
 
 // Fused: token-major projections q_src [B, L, Hq*D], k_src/v_src [B, L, Hkv*D]
 // -> q_out [B, Hq, L, D] rotated, cache K[b,h,pos0+l,:] rotated, V copied.
-// One thread per (b, l, head in Hq + 2*Hkv, i < D/2).
+// A thread owns (b, l, i < D/2) and the heads h = blockIdx.y + k * gridDim.y
+// of the Hq + 2*Hkv (q, then k, then v): (cos, sin) of (pos, i) is computed
+// once for all its heads, and a wave touches 128 contiguous bytes per head.
 template <typename TS, typename TC>
 __global__ void rope_kv_fused(const TS* __restrict__ qs, const TS* __restrict__ ks,
                               const TS* __restrict__ vs, int B, int Hq, int Hkv, int L, int D,
@@ -66,31 +70,30 @@ __global__ void rope_kv_fused(const TS* __restrict__ qs, const TS* __restrict__ 
   if (dpos) pos0 = *dpos;
   const int half = D / 2;
   const int NH = Hq + 2 * Hkv;
-  const int64_t total = (int64_t)B * L * NH * half;
+  const int64_t total = (int64_t)B * L * half;
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
     const int i = idx % half;
-    int64_t r = idx / half;
-    const int h = r % NH;
-    r /= NH;
+    const int64_t r = idx / half;
     const int l = r % L;
     const int b = r / L;
     const int pos = pos0 + l;
-    if (h < Hq + Hkv) {
-      float c, s;
-      rope_cs(pos, i, D, theta, &c, &s);
-      float o1, o2;
+    float c = 0.f, s = 0.f;
+    if ((int)blockIdx.y < Hq + Hkv) rope_cs(pos, i, D, theta, &c, &s);
+    for (int h = blockIdx.y; h < NH; h += gridDim.y) {
       if (h < Hq) {
         const int64_t so = ((int64_t)b * L + l) * Hq * D + (int64_t)h * D;
+        float o1, o2;
         rotate_pair(Elem<TS>::load(qs, so + i), Elem<TS>::load(qs, so + i + half), c, s, &o1, &o2);
         const int64_t oo = (((int64_t)b * Hq + h) * L + l) * D;
         Elem<TS>::store(q_out, oo + i, o1);
         Elem<TS>::store(q_out, oo + i + half, o2);
-      } else {
+      } else if (h < Hq + Hkv) {
         const int hk = h - Hq;
         const int64_t so = ((int64_t)b * L + l) * Hkv * D + (int64_t)hk * D;
         // K is rotated in the source dtype first (the projection output
         // dtype), then stored in the cache dtype.
+        float o1, o2;
         rotate_pair(Elem<TS>::load(ks, so + i), Elem<TS>::load(ks, so + i + half), c, s, &o1, &o2);
         if constexpr (sizeof(TS) == 2) {
           o1 = bf16_to_f32(f32_to_bf16(o1));
@@ -99,13 +102,13 @@ __global__ void rope_kv_fused(const TS* __restrict__ qs, const TS* __restrict__ 
         const int64_t co = (((int64_t)b * Hkv + hk) * Lmax + pos) * D;
         Elem<TC>::store(kc, co + i, o1);
         Elem<TC>::store(kc, co + i + half, o2);
+      } else {
+        const int hv = h - Hq - Hkv;
+        const int64_t so = ((int64_t)b * L + l) * Hkv * D + (int64_t)hv * D;
+        const int64_t co = (((int64_t)b * Hkv + hv) * Lmax + pos) * D;
+        Elem<TC>::store(vc, co + i, Elem<TS>::load(vs, so + i));
+        Elem<TC>::store(vc, co + i + half, Elem<TS>::load(vs, so + i + half));
       }
-    } else {
-      const int hv = h - Hq - Hkv;
-      const int64_t so = ((int64_t)b * L + l) * Hkv * D + (int64_t)hv * D;
-      const int64_t co = (((int64_t)b * Hkv + hv) * Lmax + pos) * D;
-      Elem<TC>::store(vc, co + i, Elem<TS>::load(vs, so + i));
-      Elem<TC>::store(vc, co + i + half, Elem<TS>::load(vs, so + i + half));
     }
   }
 }
@@ -163,8 +166,13 @@ int strata_rope_kv_fused_launch(const void* qs, const void* ks, const void* vs, 
                                 const int* dpos, float theta, void* q_out, void* kc, void* vc,
                                 int cache_dtype, void* stream) {
   hipStream_t s = as_stream(stream);
-  const int64_t n = (int64_t)B * L * (Hq + 2 * Hkv) * (D / 2);
-  const dim3 g(grid_for(n)), blk(256);
+  // Heads are dealt over grid.y: all of them for short inputs (as many
+  // threads as elements), slices of 6 from 256 rows, so (cos, sin) is
+  // computed once per 6 heads.
+  const int NH = Hq + 2 * Hkv;
+  const int64_t rows = (int64_t)B * L;
+  const int hy = rows >= 256 ? std::max(1, (NH + 5) / 6) : NH;
+  const dim3 g(grid_for(rows * (D / 2)), hy), blk(256);
   if (src_dtype == STRATA_BF16 && cache_dtype == STRATA_BF16)
     hipLaunchKernelGGL((rope_kv_fused<bf16_t, bf16_t>), g, blk, 0, s, (const bf16_t*)qs,
                        (const bf16_t*)ks, (const bf16_t*)vs, B, Hq, Hkv, L, D, Lmax, pos0, dpos, theta,
