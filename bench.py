@@ -55,7 +55,7 @@ def parse():
     p.add_argument("--gemv-iters", type=int, default=50)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
-    p.add_argument("--profile", choices=["gemv", "prefill"], default=None)
+    p.add_argument("--profile", choices=["gemv", "prefill", "midrows"], default=None)
     return p.parse_args()
 
 
@@ -191,6 +191,28 @@ def profile_prefill(iters=3):
     print(json.dumps({"profile": "prefill", "iters": iters,
                       "attention_flops": 4 * 32 * 128 * L * (L + 1) // 2,
                       "gate_gemm_flops": 2 * L * 14336 * 4096}))
+
+
+def profile_midrows(rows=(128, 200), iters=3):
+    """The 8B layer's prefill linears as the engine launches them (q/k/v
+    together, o, gate/up together, down) at a few mid-size row counts, each
+    ``iters`` times (for rocprofv3 kernel traces of the split-K GEMM)."""
+    import torch
+    from lokahi_amd import ops
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(5)
+    groups = [("qkv", (4096, 1024, 1024), 4096), ("o", (4096,), 4096),
+              ("gate_up", (14336, 14336), 4096), ("down", (4096,), 14336)]
+    ws = {name: [ops.quantize(torch.randn((n, k), generator=g, device=dev) * 0.02) for n in ns]
+          for name, ns, k in groups}
+    for M in rows:
+        for name, ns, k in groups:
+            x = torch.randn((M, k), generator=g, device=dev).to(torch.bfloat16)
+            outs = [torch.empty((M, n), dtype=torch.bfloat16, device=dev) for n in ns]
+            for _ in range(iters):
+                ops.linear_multi(x, ws[name], outs=outs)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": "midrows", "rows": list(rows), "iters": iters}))
 
 
 def attention_decode():
@@ -478,6 +500,9 @@ def main():
         return
     if args.profile == "prefill":
         profile_prefill()
+        return
+    if args.profile == "midrows":
+        profile_midrows()
         return
     from lokahi_amd.llama import LLAMA3_8B
 
