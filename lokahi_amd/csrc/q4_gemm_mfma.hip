@@ -386,19 +386,25 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
       }
 }
 
-// y[m, c] = sum over slices s = 0 .. S - 1, in that order, of
-// part[s][m][col0 + c], for one linear's ncols columns (a multiple of 4)
-// inside partial rows ld columns wide; four columns per thread.
+// One launch's split linears, after its slices: y_p[m, c] = sum over
+// slices s = 0 .. S - 1, in that order, of part[s][m][n0_p - c0 + c], where
+// the launch covered columns c0 .. c0 + ld of the concatenated linears (each
+// N a multiple of 256); four columns per thread.
 template <typename YT>
 __global__ __launch_bounds__(256) void q4_gemm_splitk_reduce(const float* __restrict__ part, int S,
-                                                             int64_t slice, int ld, int col0, int M,
-                                                             int ncols, YT* __restrict__ y) {
-  const int c4 = ncols >> 2;
+                                                             int64_t slice, int ld, int c0, int M,
+                                                             GemmOut out) {
+  const int c4 = ld >> 2;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)M * c4) return;
   const int64_t m = i / c4;
-  const int64_t c = (i - m * c4) * 4;
-  const float* pp = part + m * ld + col0 + c;
+  const int c = (int)(i - m * c4) * 4;  // column in the launch
+  int p = 0;
+#pragma unroll
+  for (int t = 1; t < kMaxGemmProblems; ++t)
+    if (t < out.count && c0 + c >= out.n0[t]) p = t;
+  const int np = out.n0[p + 1] - out.n0[p], cp = c0 + c - out.n0[p];
+  const float* pp = part + m * ld + c;
   float4 a = *reinterpret_cast<const float4*>(pp);
   for (int s = 1; s < S; ++s) {
     const float4 b = *reinterpret_cast<const float4*>(pp + s * slice);
@@ -407,7 +413,8 @@ __global__ __launch_bounds__(256) void q4_gemm_splitk_reduce(const float* __rest
     a.z += b.z;
     a.w += b.w;
   }
-  const int64_t off = m * ncols + c;
+  YT* y = static_cast<YT*>(out.y[p]);
+  const int64_t off = m * np + cp;
   Elem<YT>::store(y, off, a.x);
   Elem<YT>::store(y, off + 1, a.y);
   Elem<YT>::store(y, off + 2, a.z);
@@ -617,8 +624,8 @@ int strata_q4_gemm_mfma_run(const void* x, int M, int K, const void* packed,
   SplitPlan pl = split_plan(M, K, ws, count, cus, part != nullptr);
   if (plan_part_bytes(pl, M, ws) > part_bytes) pl = split_plan(M, K, ws, count, cus, false);
   // One launch per run of linears with the same slice count; a split run is
-  // followed by the in-order sum of its slices per linear (the partial
-  // buffer is reused run after run, in stream order).
+  // followed by one launch that sums its slices in order for all of its
+  // linears (the partial buffer is reused run after run, in stream order).
   for (int r = 0; r < pl.runs; ++r) {
     const int pa = pl.first[r], pe = pl.first[r + 1], S = pl.S[pa];
     const int c0 = out.n0[pa], ncols = out.n0[pe] - c0;
@@ -626,16 +633,13 @@ int strata_q4_gemm_mfma_run(const void* x, int M, int K, const void* packed,
     if (S == 1) continue;
     STRATA_HIP_CHECK(hipGetLastError());
     const int64_t slice = (int64_t)((M + 127) / 128 * 128) * ncols;
-    for (int p = pa; p < pe; ++p) {
-      const int np = (int)ws[p].N;
-      const unsigned blocks = (unsigned)(((int64_t)M * (np / 4) + 255) / 256);
-      if (bf)
-        hipLaunchKernelGGL(q4_gemm_splitk_reduce<bf16_t>, dim3(blocks), dim3(256), 0, st, part, S,
-                           slice, ncols, out.n0[p] - c0, M, np, static_cast<bf16_t*>(ws[p].y));
-      else
-        hipLaunchKernelGGL(q4_gemm_splitk_reduce<float>, dim3(blocks), dim3(256), 0, st, part, S,
-                           slice, ncols, out.n0[p] - c0, M, np, static_cast<float*>(ws[p].y));
-    }
+    const unsigned blocks = (unsigned)(((int64_t)M * (ncols / 4) + 255) / 256);
+    if (bf)
+      hipLaunchKernelGGL(q4_gemm_splitk_reduce<bf16_t>, dim3(blocks), dim3(256), 0, st, part, S,
+                         slice, ncols, c0, M, out);
+    else
+      hipLaunchKernelGGL(q4_gemm_splitk_reduce<float>, dim3(blocks), dim3(256), 0, st, part, S,
+                         slice, ncols, c0, M, out);
   }
   STRATA_HIP_CHECK(hipGetLastError());
   return STRATA_OK;
