@@ -205,14 +205,17 @@ def test_gemm_few_rows_skinny_kernel(dev, M, K):
 @pytest.mark.parametrize("M,K,ns", [(65, 4096, (4096, 1024, 1024)), (100, 1024, (1024, 256, 256)),
                                     (128, 4096, (14336,)), (200, 14336, (4096,)),
                                     (255, 2048, (512, 1536)), (300, 1024, (1024, 256, 256)),
-                                    (777, 4096, (4096,))])
+                                    (777, 4096, (4096,)), (128, 4096, (14336, 4096)),
+                                    (40, 512, (256,)), (1000, 64, (256, 512))])
 def test_gemm_mid_rows_split_k(dev, M, K, ns):
     """40 rows and up, N a multiple of 256: the 256-column MFMA
     kernel over all rows (a partial last row tile), each linear whose tiles
     leave CUs idle split over K slices whose fp32 partial sums are added in
     slice order.  Against x @ bf16(dequant(W)).T in float64 and the oracle's
     q4 matmul; a linear gives the same bits in a fused launch as alone (the
-    split depends on its own M, K and N only)."""
+    split depends on its own M, K and N only).  Includes a call whose
+    linears get different slice counts (two launches), K = 64 (one group,
+    no split) and exactly 40 rows at a short K."""
     from lokahi_amd import ops
     rng = np.random.default_rng(M * 11 + K)
     probs = [_problem(rng, n, K)[:3] for n in ns]
