@@ -134,7 +134,10 @@ struct GemmSplit {
   float* part;
 };
 
-template <int TM, typename YT>
+// SPLIT: the launch's K slices write fp32 partial sums (sp.part) instead
+// of the outputs; a separate instance, so the other one carries no partial
+// pointer arithmetic (it spilled to scratch when it did).
+template <int TM, typename YT, bool SPLIT>
 __global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(TM == 256 ? 1 : 2, TM == 256 ? 1 : 2)))
 void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
                          const uint32_t* __restrict__ wt, const uint32_t* __restrict__ sbt,
@@ -354,7 +357,7 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
     stg = stg1;
   }
   // C layout: lane holds column c32, rows 8 (i / 4) + 4 kh + i % 4.
-  if (sp.part) {  // this K slice's fp32 partial sums, every row of the tile
+  if constexpr (SPLIT) {  // this K slice's fp32 partial sums, every row of the tile
     const int ld = nts * TN;
     float* pb = sp.part + ((int64_t)ks * (mt * TM) + m0 + 4 * kh) * ld + tnl * TN + wave * WN + c32;
 #pragma unroll
@@ -364,8 +367,7 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
 #pragma unroll
         for (int i = 0; i < 16; ++i)
           pb[(int64_t)(mb * 32 + 8 * (i / 4) + i % 4) * ld + nb * 32] = acc[mb][nb][i];
-    return;
-  }
+  } else {
   // The tile's problem (wave-uniform): the last one starting at or before n0.
   int p = 0;
 #pragma unroll
@@ -374,16 +376,28 @@ void q4_gemm_mfma_kernel(const uint16_t* __restrict__ x, int M, int K,
   const int np = out.n0[p + 1] - out.n0[p];
   YT* yb = static_cast<YT*>(out.y[p]) + (int64_t)(m0 + 4 * kh) * np + (n0 - out.n0[p]) +
            wave * WN + c32;
-  const int rows_left = M - (m0 + 4 * kh);  // rows of a partial last tile are not stored
+  if (m0 + TM <= M) {  // a full tile (wave-uniform): stores without a row check
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = mb * 32 + 8 * (i / 4) + i % 4;
-        if (r < rows_left) Elem<YT>::store(yb, (int64_t)r * np + nb * 32, acc[mb][nb][i]);
-      }
+        for (int i = 0; i < 16; ++i)
+          Elem<YT>::store(yb, (int64_t)(mb * 32 + 8 * (i / 4) + i % 4) * np + nb * 32,
+                          acc[mb][nb][i]);
+  } else {  // the partial last tile: rows at or past M are not stored
+    const int rows_left = M - (m0 + 4 * kh);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int r = mb * 32 + 8 * (i / 4) + i % 4;
+          if (r < rows_left) Elem<YT>::store(yb, (int64_t)r * np + nb * 32, acc[mb][nb][i]);
+        }
+  }
+  }
 }
 
 // One launch's split linears, after its slices: y_p[m, c] = sum over
@@ -563,16 +577,16 @@ size_t plan_part_bytes(const SplitPlan& pl, int M, const strata_q4_weight* ws) {
   return need;
 }
 
-template <int TM, typename YT>
+template <int TM, typename YT, bool SPLIT>
 void gemm_go(const void* x, int M, int K, const uint32_t* wt, const uint32_t* sbt, int N,
              const GemmOut& out, const GemmSplit& sp, hipStream_t st) {
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void*)q4_gemm_mfma_kernel<TM, YT>,
+    (void)hipFuncSetAttribute((const void*)q4_gemm_mfma_kernel<TM, YT, SPLIT>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, Tile<TM>::kLds);
     attr = true;
   }
-  hipLaunchKernelGGL((q4_gemm_mfma_kernel<TM, YT>), dim3(sp.mt * sp.nts * sp.S), dim3(NTHR),
+  hipLaunchKernelGGL((q4_gemm_mfma_kernel<TM, YT, SPLIT>), dim3(sp.mt * sp.nts * sp.S), dim3(NTHR),
                      Tile<TM>::kLds, st, (const uint16_t*)x, M, K, wt, sbt, N, out, sp);
 }
 }  // namespace
@@ -613,12 +627,14 @@ int strata_q4_gemm_mfma_run(const void* x, int M, int K, const void* packed,
     const bool big = S == 1 && (int64_t)((M + 255) / 256) * nts >= 2 * cus;
     const int TM = big ? 256 : 128;
     const GemmSplit sp{(M + TM - 1) / TM, ntile0, nts, S, S > 1 ? part : nullptr};
-    if (big) {
-      if (bf) gemm_go<256, bf16_t>(x, M, K, wt, sbt, N, out, sp, st);
-      else gemm_go<256, float>(x, M, K, wt, sbt, N, out, sp, st);
+    if (S > 1)  // 128-row tiles; the partial sums are fp32 whatever y's dtype
+      gemm_go<128, float, true>(x, M, K, wt, sbt, N, out, sp, st);
+    else if (big) {
+      if (bf) gemm_go<256, bf16_t, false>(x, M, K, wt, sbt, N, out, sp, st);
+      else gemm_go<256, float, false>(x, M, K, wt, sbt, N, out, sp, st);
     } else {
-      if (bf) gemm_go<128, bf16_t>(x, M, K, wt, sbt, N, out, sp, st);
-      else gemm_go<128, float>(x, M, K, wt, sbt, N, out, sp, st);
+      if (bf) gemm_go<128, bf16_t, false>(x, M, K, wt, sbt, N, out, sp, st);
+      else gemm_go<128, float, false>(x, M, K, wt, sbt, N, out, sp, st);
     }
   };
   SplitPlan pl = split_plan(M, K, ws, count, cus, part != nullptr);
