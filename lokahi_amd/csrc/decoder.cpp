@@ -1,6 +1,7 @@
 // Native Llama decoder engine: forward passes and greedy generation launched
-// from C++ over the library's kernels, with the decode step captured once as
-// a HIP graph and replayed per token.
+// from C++ over the library's kernels.  Decode steps are launched from the
+// host per token, or captured once per context bucket as a HIP graph and
+// replayed (use_graph).
 //
 // Follows MLXLlamaForCausalLM.__call__ (src/ollm/llama_mlx.py:863-912),
 // MLXLlamaModel.__call__ (740-833), MLXLlamaDecoderLayer.__call__ (608-658),
