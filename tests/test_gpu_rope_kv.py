@@ -120,3 +120,36 @@ def test_fused_rope_kv_append_matches_oracle(dev):
         assert np.array_equal(bits(V), f32_to_bf16_bits(rv))
         pos0 += L
     assert cache.get_seq_length(0) == 7
+
+
+def test_fused_rope_kv_append_long_rows_matches_oracle(dev):
+    """From 256 rows (B * L) the fused kernel deals each thread a slice of
+    the heads and computes (cos, sin) once per slice; 8B geometry (32 q / 8
+    KV heads, D 128, theta 5e5) at B = 2, L = 300 then a one-token append,
+    bit-exact against the oracle."""
+    from types import SimpleNamespace
+    from lokahi_amd.kvcache import HipKVCache
+    B, Hq, Hkv, D, theta = 2, 32, 8, 128, 500000.0
+    cfg = SimpleNamespace(num_hidden_layers=1, num_key_value_heads=Hkv, num_attention_heads=Hq,
+                          hidden_size=Hq * D)
+    rng = np.random.default_rng(5)
+    cache = HipKVCache(cfg, batch_size=B, max_length=320, dtype=torch.bfloat16)
+    ref = OracleKVCache(1)
+    pos0 = 0
+    for L in (300, 1):
+        q = round_bf16(rng.normal(size=(B, L, Hq * D)).astype(np.float32))
+        k = round_bf16(rng.normal(size=(B, L, Hkv * D)).astype(np.float32))
+        v = round_bf16(rng.normal(size=(B, L, Hkv * D)).astype(np.float32))
+        qo = torch.empty((B, Hq, L, D), dtype=torch.bfloat16, device=dev)
+        cache.rope_append(0, bf16_dev(q, dev), bf16_dev(k, dev), bf16_dev(v, dev), Hq, L, theta, qo)
+        c, s = rope.cos_sin(np.arange(pos0, pos0 + L)[None], D, theta)
+        qh = q.reshape(B, L, Hq, D).transpose(0, 2, 1, 3)
+        kh = k.reshape(B, L, Hkv, D).transpose(0, 2, 1, 3)
+        vh = v.reshape(B, L, Hkv, D).transpose(0, 2, 1, 3)
+        assert np.array_equal(bits(qo), f32_to_bf16_bits(rope.apply(qh, c, s)))
+        rk, rv = ref.update(round_bf16(rope.apply(kh, c, s)), vh, 0)
+        K, V = cache.views(0)
+        assert np.array_equal(bits(K), f32_to_bf16_bits(rk))
+        assert np.array_equal(bits(V), f32_to_bf16_bits(rv))
+        pos0 += L
+    assert cache.get_seq_length(0) == 301
