@@ -624,7 +624,8 @@ int strata_q4_gemm_mfma_run(const void* x, int M, int K, const void* packed,
   // A launch over columns [ntile0, ntile0 + nts) tiles with S slices: 256-row
   // tiles unless that leaves the GPU under two workgroups per CU.
   auto go = [&](int ntile0, int nts, int S) {
-    const bool big = S == 1 && (int64_t)((M + 255) / 256) * nts >= 2 * cus;
+    bool big = S == 1 && (int64_t)((M + 255) / 256) * nts >= 2 * cus;
+    if (const char* e = getenv("STRATA_GEMM_TM")) big = S == 1 && atoi(e) == 256;  // timing runs
     const int TM = big ? 256 : 128;
     const GemmSplit sp{(M + TM - 1) / TM, ntile0, nts, S, S > 1 ? part : nullptr};
     if (S > 1)  // 128-row tiles; the partial sums are fp32 whatever y's dtype
