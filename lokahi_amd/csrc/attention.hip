@@ -1189,7 +1189,9 @@ constexpr int kBatchedShortKeys = 2048; // batched heads: 2 per CU up to here
 constexpr int kBatchedLongKeys = 16384; // batched heads: 6 per CU from here
 void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
   int min_chunk = Lcap >= kLongSplitKeys ? 128 : 64;
-  if (const char* e = getenv("STRATA_ATTN_MIN_CHUNK")) min_chunk = std::max(64, atoi(e));
+  // Overrides (timing runs) are read once per process: this runs per launch.
+  static const char* const env_min_chunk = getenv("STRATA_ATTN_MIN_CHUNK");
+  if (const char* e = env_min_chunk) min_chunk = std::max(64, atoi(e));
   // Batched heads (B*Hkv >= 64, e.g. 16 x 8): short contexts prefer longer
   // splits (1k keys: 21.6 us at 2 per CU against 24.0 at 4), very long ones
   // more of them (32k keys: 371 us at 6 against 378 at 4).  Few heads (batch
@@ -1234,7 +1236,8 @@ inline bool mfma_decode(int B, int Hkv, int64_t L) {
 constexpr int kMfmaDecodeWaves = 4;  // waves per workgroup (each with its own LDS ring)
 void decode_mfma_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
   int per_cu = 4;
-  if (const char* e = getenv("STRATA_ATTN_MFMA_WAVES_PER_CU")) per_cu = std::max(1, atoi(e));
+  static const char* const env_mfma_waves = getenv("STRATA_ATTN_MFMA_WAVES_PER_CU");  // once
+  if (const char* e = env_mfma_waves) per_cu = std::max(1, atoi(e));
   int ns = (num_cus * per_cu + B * Hkv - 1) / (B * Hkv);
   ns = std::max(1, std::min(ns, std::min(kMaxDecodeSplits, (Lcap + 63) / 64)));
   int chunk = (Lcap + ns - 1) / ns;
