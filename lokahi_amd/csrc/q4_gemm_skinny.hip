@@ -1,4 +1,4 @@
-// q4 linear for a few rows (9 <= M <= 64 on the default path): Y[M, N] =
+// q4 linear for a few rows (9 <= M < 40 on the default path, up to 64): Y[M, N] =
 // X[M, K] @ dequant(W)[N, K]^T on bf16 16x16x32 MFMAs, every weight read once.
 //
 // Same maths as mx.quantized_matmul(transpose=True) (src/ollm/llama_mlx.py:
