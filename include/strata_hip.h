@@ -95,6 +95,27 @@ int strata_linear_q4_multi(strata_ctx* ctx, const void* x, int x_dtype, int64_t 
                            int64_t K, const strata_q4_weight* weights, int count,
                            int group_size, int bits, int y_dtype, void* stream);
 
+/* Decode linears over a load-time weight layout.  The reference places each
+ * layer's quantized tensors on the device once when it loads the layer
+ * (`_load_layer_weights` / `_assign_layer_weight`,
+ * src/ollm/llama_mlx.py:498-580) and every step then runs `_linear` on them
+ * (53-74).  strata_q4_layout_create is that load step for linears sharing x
+ * (q/k/v, or gate/up): it copies the MLX-layout triples into the layout the
+ * matrix-core decode GEMV streams (16-row blocks, scale and bias packed next
+ * to the codes, K padded to a multiple of 1024); the MLX tensors may be
+ * freed afterwards.  strata_linear_q4_layout then computes
+ * y_i = x @ (scales_i*q_i + biases_i).T for 1 <= M <= 4 bf16 rows, fp32
+ * accumulate, y_dtype f32 or bf16 (ys[i] is [M, N_i]).
+ * Requirements: K % 64 == 0, K <= 16384, count 1..8, group_size 64, 4 bits.
+ * The layout is read-only after creation: calls may share it. */
+typedef struct strata_q4_layout strata_q4_layout;
+int strata_q4_layout_create(strata_ctx* ctx, const strata_q4_weight* weights, int count,
+                            int64_t K, strata_q4_layout** out);
+int strata_q4_layout_destroy(strata_q4_layout* layout);
+int strata_linear_q4_layout(strata_ctx* ctx, const void* x, int x_dtype, int64_t M,
+                            const strata_q4_layout* layout, void* const* ys, int y_dtype,
+                            void* stream);
+
 /* Dense bf16-weight linear y = x @ W.T, W [N, K] bf16, fp32 accumulate.
  * Replaces the unquantized `_linear` branch `mx.matmul(x, weight.T)`
  * (src/ollm/llama_mlx.py:64-65) used for the bf16 lm_head (886-910). */

@@ -153,6 +153,57 @@ int strata_linear_q4(strata_ctx* ctx, const void* x, int x_dtype, int64_t M, int
   return strata_linear_q4_multi(ctx, x, x_dtype, M, K, &wt, 1, group_size, bits, y_dtype, stream);
 }
 
+struct strata_q4_layout {
+  GemvLayout L;
+};
+
+int strata_q4_layout_create(strata_ctx* ctx, const strata_q4_weight* weights, int count, int64_t K,
+                            strata_q4_layout** out) {
+  STRATA_REQUIRE(ctx != nullptr && weights != nullptr && out != nullptr, "null argument");
+  STRATA_REQUIRE(count >= 1 && count <= 8, "count must be in 1..8 (got %d)", count);
+  STRATA_REQUIRE(K > 0 && K % 64 == 0 && K <= 16384,
+                 "K=%lld must be a positive multiple of 64, at most 16384", (long long)K);
+  for (int i = 0; i < count; ++i) {
+    const strata_q4_weight& wt = weights[i];
+    STRATA_REQUIRE(wt.N > 0 && wt.N <= (1 << 24) && wt.w && wt.scales && wt.biases,
+                   "weight %d: null pointer or N outside 1..2^24", i);
+  }
+  auto* h = new strata_q4_layout{};
+  const int rc = strata_gemv_layout_build(weights, count, (int)K, 0, 0, &h->L, nullptr);
+  if (rc) {
+    delete h;
+    return rc;
+  }
+  if (hipStreamSynchronize(nullptr) != hipSuccess) {
+    strata_gemv_layout_free(&h->L);
+    delete h;
+    return strata_set_error(STRATA_EHIP, "layout: re-layout kernels failed");
+  }
+  *out = h;
+  return STRATA_OK;
+}
+
+int strata_q4_layout_destroy(strata_q4_layout* layout) {
+  if (!layout) return STRATA_OK;
+  strata_gemv_layout_free(&layout->L);
+  delete layout;
+  return STRATA_OK;
+}
+
+int strata_linear_q4_layout(strata_ctx* ctx, const void* x, int x_dtype, int64_t M,
+                            const strata_q4_layout* layout, void* const* ys, int y_dtype,
+                            void* stream) {
+  STRATA_REQUIRE(ctx != nullptr && layout != nullptr && x != nullptr && ys != nullptr,
+                 "null argument");
+  STRATA_REQUIRE(x_dtype == STRATA_BF16, "the layout GEMV takes bf16 activations");
+  STRATA_REQUIRE(dtype_ok(y_dtype), "unknown dtype code");
+  STRATA_REQUIRE(M >= 0 && M <= 4, "M=%lld outside 0..4", (long long)M);
+  STRATA_REQUIRE(aligned16(x), "x must be 16-byte aligned");
+  for (int i = 0; i < layout->L.count; ++i) STRATA_REQUIRE(ys[i] != nullptr, "output %d is NULL", i);
+  if (M == 0) return STRATA_OK;
+  return strata_gemv_layout_run(layout->L, x, (int)M, ys, y_dtype, nullptr, stream);
+}
+
 int strata_linear_bf16(strata_ctx* ctx, const void* x, int x_dtype, int64_t M, int64_t K,
                        const uint16_t* w, int64_t N, void* y, int y_dtype, void* stream) {
   STRATA_REQUIRE(ctx != nullptr, "ctx is NULL");

@@ -27,6 +27,29 @@ struct GemvEpilogue {
   const float2* rope_table;  // (cos, sin) table [lmax][head_dim/2], required by mode 2
   const float2* rope_cur;    // with dpos: (cos, sin) [head_dim/2] of position *dpos
 };
+// Decode GEMV over the load-time "GEMV layout" (q4_gemv_mfma.hip): the
+// linears of one launch re-laid out once into 16-row blocks for the 16x16x32
+// bf16 matrix-core kernel.  perm: 0 rows in order (store / residual
+// epilogues), 1 gate/up pairs (SiLU epilogue; ws = {gate, up}), 2 rotate-half
+// pairs inside heads of head_dim rows (RoPE + KV append; ws = {q, k, v}).
+constexpr int kGvMaxProblems = 8;
+struct GemvLayout {
+  void* buf = nullptr;  // codes, then the packed (scale, bias) words
+  size_t code_bytes = 0, sb_bytes = 0;
+  int K = 0, nt = 0, nrb = 0, perm = 0, head_dim = 0;
+  int count = 0;                      // output problems (1 for perm 1)
+  int rb0[kGvMaxProblems + 1] = {};  // first row block of each problem
+  int64_t N[kGvMaxProblems] = {};     // output rows of each problem
+};
+// K % 64 == 0, K <= 16384 and 1 <= M <= 4.
+bool strata_gemv_layout_fits(int K, int M);
+int strata_gemv_layout_build(const strata_q4_weight* ws, int count, int K, int perm, int head_dim,
+                             GemvLayout* out, void* stream);
+void strata_gemv_layout_free(GemvLayout* L);
+// bf16 x [M, K]; ys[i] is problem i's output (perm 1: act [M, N]); e (may be
+// null) selects the prologue/epilogue as for strata_q4_gemv_epi.
+int strata_gemv_layout_run(const GemvLayout& L, const void* x, int M, void* const* ys, int y_dtype,
+                           const GemvEpilogue* e, void* stream);
 int strata_q4_gemv_epi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
                        int count, const GemvEpilogue& e, void* stream);
 int strata_q4_gemv_resid(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,

@@ -126,6 +126,62 @@ def linear_multi(x: torch.Tensor, weights: Sequence[Tuple[torch.Tensor, torch.Te
     return [y.reshape(*lead, y.shape[-1]) for y in ys]
 
 
+class Q4Layout:
+    """Linears sharing ``x`` copied once into the decode GEMV's load-time
+    layout (``strata_q4_layout_create``; the reference's load step is
+    ``_load_layer_weights``, ``src/ollm/llama_mlx.py:550-580``).  Calling it
+    runs ``_linear`` on each of them (``llama_mlx.py:53-74``) for 1..4 bf16
+    rows of ``x`` on the matrix-core GEMV."""
+
+    def __init__(self, weights: Sequence[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]],
+                 *, group_size: int = 64, bits: int = 4):
+        if not weights:
+            raise ValueError("at least one weight is required")
+        K = weights[0][0].shape[1] * 8
+        self.device = _dev(weights[0][0])
+        self.K = K
+        self.N = []
+        arr = (_abi.Q4Weight * len(weights))()
+        for i, (w, s, b) in enumerate(weights):
+            N = w.shape[0]
+            _check_q4(w, s, b, N, K, group_size, bits)
+            self.N.append(N)
+            arr[i] = _abi.Q4Weight(w.data_ptr(), s.data_ptr(), b.data_ptr(), N, None)
+        torch.cuda.synchronize(self.device)
+        h = C.c_void_p()
+        check(_lib().strata_q4_layout_create(_ctx(self.device), arr, len(weights), K, C.byref(h)))
+        self._h = h
+
+    def __call__(self, x: torch.Tensor, *, outs: Optional[Sequence[torch.Tensor]] = None,
+                 out_dtype: Optional[torch.dtype] = None):
+        if self._h is None:
+            raise ValueError("layout is closed")
+        if x.dtype != torch.bfloat16 or x.shape[-1] != self.K:
+            raise ValueError(f"x must be bf16 [..., {self.K}]")
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.K).contiguous()
+        M = x2.shape[0]
+        out_dtype = out_dtype or torch.bfloat16
+        ys = list(outs) if outs is not None else [
+            torch.empty((M, n), dtype=out_dtype, device=x.device) for n in self.N]
+        ptrs = (C.c_void_p * len(ys))(*[y.data_ptr() for y in ys])
+        check(_lib().strata_linear_q4_layout(_ctx(self.device), x2.data_ptr(), BF16, M, self._h,
+                                             ptrs, _code(ys[0]), _stream(self.device)))
+        return [y.reshape(*lead, y.shape[-1]) for y in ys]
+
+    def close(self):
+        if getattr(self, "_h", None) is not None:
+            torch.cuda.synchronize(self.device)
+            _lib().strata_q4_layout_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def quantize(weight: torch.Tensor, group_size: int = 64):
     """Quantize a float32/bf16 ``[N, K]`` device tensor to (u32 packed, bf16 scales, bf16 biases)."""
     dev = _dev(weight)
