@@ -61,6 +61,11 @@ struct strata_decoder {
   // Prefill GEMM layout of each layer's launches (q/k/v, o, gate/up, down),
   // re-laid out once at creation (null: re-laid out per call).
   std::vector<void*> packed;
+  // Decode GEMV layout of the same launches (4 per layer, q4_gemv_mfma.hip),
+  // built once at creation; empty when the model's shapes do not fit it
+  // (the decode step then runs the MLX-layout GEMV).
+  std::vector<GemvLayout> dlay;
+  GemvLayout head_lay;  // q4 lm_head in the GEMV layout (head_q4 set)
 };
 
 namespace {
@@ -71,6 +76,10 @@ namespace {
 int lm_head_launch(strata_decoder* d, const void* x, int M, float* logits, void* stream) {
   const strata_llama_config& c = d->cfg;
   if (d->head_q4.w) {
+    if (d->head_lay.buf && M <= 4) {
+      void* ys[1] = {logits};
+      return strata_gemv_layout_run(d->head_lay, x, M, ys, STRATA_F32, nullptr, stream);
+    }
     strata_q4_weight w = d->head_q4;
     w.y = logits;
     return strata_q4_gemv(d->ctx, x, STRATA_BF16, M, c.hidden_size, &w, 1, STRATA_F32, stream);
@@ -109,6 +118,7 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
   // One-token steps (T <= 8 rows) fuse RoPE/append and SiLU into GEMV epilogues.
   const bool decode = L == 1 && T <= 8;
   if (decode) {
+    const bool use_lay = !d->dlay.empty() && T <= 4;
     // Five launches per layer; the residual stream h is updated in place by
     // the o/down epilogues, and RMSNorm runs in the q/k/v and gate/up
     // prologues:
@@ -121,12 +131,15 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
       const strata_llama_layer& Lw = d->layers[li];
       void* kc = kv->kl(li);
       void* vc = kv->vl(li);
+      const GemvLayout* lay = use_lay ? &d->dlay[(size_t)li * 4] : nullptr;
       strata_q4_weight qkv[3] = {Lw.q, Lw.k, Lw.v};
       GemvEpilogue eq{2, D, Hq, Hkv, kv->Lmax, graph_mode ? 0 : pos0,
                       graph_mode ? d->counters + 1 : nullptr, c.rope_theta,
                       (uint16_t*)d->qr, (uint16_t*)kc, (uint16_t*)vc, Lw.input_norm,
                       c.rms_norm_eps, d->rope_table, graph_mode ? d->rope_cur : nullptr};
-      RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, qkv, 3, eq, stream));
+      void* no_y[3] = {nullptr, nullptr, nullptr};
+      if (lay) RC(strata_gemv_layout_run(lay[0], d->h, T, no_y, STRATA_BF16, &eq, stream));
+      else RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, qkv, 3, eq, stream));
       AttnExtra ex;
       ex.part = d->part;
       ex.part_splits = d->part_splits;
@@ -139,15 +152,20 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
                       nullptr};
       strata_q4_weight o = Lw.o;
       o.y = d->h;
-      RC(strata_q4_gemv_epi(d->ctx, d->attn, T, Hq * D, &o, 1, er, stream));
+      void* yh[1] = {d->h};
+      if (lay) RC(strata_gemv_layout_run(lay[1], d->attn, T, yh, STRATA_BF16, &er, stream));
+      else RC(strata_q4_gemv_epi(d->ctx, d->attn, T, Hq * D, &o, 1, er, stream));
       strata_q4_weight gu[2] = {Lw.gate, Lw.up};
       gu[0].y = d->act;
       GemvEpilogue es{1, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr, Lw.post_norm,
                       c.rms_norm_eps, nullptr};
-      RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, gu, 2, es, stream));
+      void* ya[1] = {d->act};
+      if (lay) RC(strata_gemv_layout_run(lay[2], d->h, T, ya, STRATA_BF16, &es, stream));
+      else RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, gu, 2, es, stream));
       strata_q4_weight dn = Lw.down;
       dn.y = d->h;
-      RC(strata_q4_gemv_epi(d->ctx, d->act, T, F, &dn, 1, er, stream));
+      if (lay) RC(strata_gemv_layout_run(lay[3], d->act, T, yh, STRATA_BF16, &er, stream));
+      else RC(strata_q4_gemv_epi(d->ctx, d->act, T, F, &dn, 1, er, stream));
     }
     RC(strata_rmsnorm_launch(d->h, nullptr, d->final_norm, T, H, c.rms_norm_eps, d->hn, stream));
     return lm_head_launch(d, d->hn, B, d->logits, stream);
@@ -229,9 +247,12 @@ void set_lengths(strata_decoder* d, int len) {
 // prefill, in the layout of q4_gemm_relayout_kernel, when prefills can reach
 // the 256-column MFMA kernel and every linear qualifies.  Costs one more copy of the
 // q4 linears; on an allocation failure the prefill re-lays out per call.
+// STRATA_DECODER_NO_PREFILL_PACK (read once) skips it: prefills then
+// re-lay out per call and the copy's memory is not held.
 int pack_prefill_weights(strata_decoder* d) {
   const strata_llama_config& c = d->cfg;
-  if (d->max_tokens < kMfmaMidRows) return STRATA_OK;
+  static const bool skip = getenv("STRATA_DECODER_NO_PREFILL_PACK") != nullptr;
+  if (skip || d->max_tokens < kMfmaMidRows) return STRATA_OK;
   const int H = c.hidden_size, F = c.intermediate_size, QW = c.num_heads * c.head_dim;
   std::vector<void*> packed;
   for (const strata_llama_layer& L : d->layers) {
@@ -262,6 +283,41 @@ int pack_prefill_weights(strata_decoder* d) {
     }
   }
   d->packed.swap(packed);
+  return STRATA_OK;
+}
+
+// Load-time GEMV layout of every layer's decode launches: q/k/v (rows in
+// rotate-half pairs for the RoPE epilogue), o, gate/up (SiLU pairs), down.
+// Skipped (decode then reads the MLX layout) when a width is beyond the
+// layout kernel (K > 16384) or the head size is not a multiple of 16.
+// STRATA_DECODER_NO_GEMV_LAYOUT (read per decoder creation) keeps the MLX
+// layout for decode.
+int build_decode_layouts(strata_decoder* d) {
+  const strata_llama_config& c = d->cfg;
+  if (getenv("STRATA_DECODER_NO_GEMV_LAYOUT") != nullptr) return STRATA_OK;
+  const int H = c.hidden_size, F = c.intermediate_size, QW = c.num_heads * c.head_dim;
+  if (!strata_gemv_layout_fits(H, 1) || !strata_gemv_layout_fits(F, 1) ||
+      !strata_gemv_layout_fits(QW, 1) || c.head_dim % 16 != 0)
+    return STRATA_OK;
+  std::vector<GemvLayout> lays;
+  auto fail = [&](int rc) {
+    for (GemvLayout& L : lays) strata_gemv_layout_free(&L);
+    return rc;
+  };
+  for (const strata_llama_layer& L : d->layers) {
+    const strata_q4_weight qkv[3] = {L.q, L.k, L.v}, gu[2] = {L.gate, L.up};
+    GemvLayout g[4];
+    int rc = strata_gemv_layout_build(qkv, 3, H, 2, c.head_dim, &g[0], nullptr);
+    if (!rc) rc = strata_gemv_layout_build(&L.o, 1, QW, 0, 0, &g[1], nullptr);
+    if (!rc) rc = strata_gemv_layout_build(gu, 2, H, 1, 0, &g[2], nullptr);
+    if (!rc) rc = strata_gemv_layout_build(&L.down, 1, F, 0, 0, &g[3], nullptr);
+    for (GemvLayout& x : g)
+      if (x.buf) lays.push_back(x);
+    if (rc) return fail(rc);
+  }
+  if (hipDeviceSynchronize() != hipSuccess)
+    return fail(strata_set_error(STRATA_EHIP, "decoder: GEMV re-layout failed"));
+  d->dlay.swap(lays);
   return STRATA_OK;
 }
 
@@ -326,6 +382,7 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
     rc = alloc(reinterpret_cast<void**>(&d->part),
                (size_t)kv->B * c.num_heads * part_stride(d->part_splits, c.head_dim) * 4);
   if (!rc) rc = pack_prefill_weights(d);
+  if (!rc) rc = build_decode_layouts(d);
   if (!rc) rc = strata_rope_table_launch(d->rope_table, kv->Lmax, c.head_dim, c.rope_theta, nullptr);
   if (!rc && hipDeviceSynchronize() != hipSuccess)
     rc = strata_set_error(STRATA_EHIP, "decoder: RoPE table initialisation failed");
@@ -344,6 +401,8 @@ int strata_decoder_destroy(strata_decoder* d) {
   hipDeviceSynchronize();
   for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
   for (void* p : d->packed) hipFree(p);
+  for (GemvLayout& L : d->dlay) strata_gemv_layout_free(&L);
+  strata_gemv_layout_free(&d->head_lay);
   void* ptrs[] = {d->h, d->xn, d->q, d->k, d->v, d->qr, d->attn, d->o, d->gate, d->up, d->act,
                   d->delta, d->hn, d->logits, d->ids, d->tokens, d->counters, d->part, d->amax,
                   d->rope_table, d->rope_cur};
@@ -363,10 +422,15 @@ int strata_decoder_set_lm_head_q4(strata_decoder* d, const strata_q4_weight* hea
   // captured decode steps hold the previous head
   STRATA_HIP_CHECK(hipStreamSynchronize(d->stream));
   for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
-  for (void* p : d->packed) hipFree(p);
   d->graphs.clear();
+  strata_gemv_layout_free(&d->head_lay);
   d->head_q4 = *head;
   d->head_q4.y = nullptr;
+  // the decode head in the GEMV layout (the MLX layout serves the rest)
+  if (!d->dlay.empty() && strata_gemv_layout_fits(d->cfg.hidden_size, 1)) {
+    RC(strata_gemv_layout_build(&d->head_q4, 1, d->cfg.hidden_size, 0, 0, &d->head_lay, nullptr));
+    STRATA_HIP_CHECK(hipDeviceSynchronize());
+  }
   return STRATA_OK;
 }
 

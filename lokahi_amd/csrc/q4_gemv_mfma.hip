@@ -49,10 +49,12 @@ namespace {
 
 constexpr uint32_t kMagic2 = 0x43004300u;  // bf16 pair (128.0, 128.0)
 
+// (w & 0x000f000f) | 0x43004300: one v_and_or_b32 with the mask in a VGPR
+// (mask_v) and the magic in an SGPR.  Plain C, not inline assembly: the
+// result feeds the matrix cores, and the compiler must see the VALU write to
+// keep the VALU -> MFMA operand hazard wait states.
 __device__ __forceinline__ uint32_t code_pair(uint32_t w, uint32_t mask_v) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(mask_v), "s"(kMagic2));
-  return r;
+  return (w & mask_v) | kMagic2;
 }
 
 __device__ __forceinline__ f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
@@ -120,6 +122,15 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   float* red = reinterpret_cast<float*>(base + nt * kWaveLds<MM>);  // [nt][MM][16]
   float* nred = red + nt * MM * 16;                                 // [nt][MM]
 
+  // the block's problem (output linear) and epilogue thread roles
+  int pi = 0;
+#pragma unroll
+  for (int q = 1; q < kGvMaxProblems; ++q)
+    if (q < a.count && rb >= a.p[q].rb0) pi = q;
+  const int lb = rb - a.p[pi].rb0;
+  const int em = threadIdx.x >> 4, er = threadIdx.x & 15;  // epilogue thread: batch row, block row
+  const bool eth = wave == 0 && em < M;
+
   // x of the task: uint4 u (0..127) = x[8u .. 8u+7] of the task, group u / 8.
   uint4 xv[MM][2], wn[2];
 #pragma unroll
@@ -137,6 +148,13 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
       const int k = 1024 * t + 8 * (lane + 64 * e);
       wn[e] = k < K ? *reinterpret_cast<const uint4*>(a.norm_w + k) : make_uint4(0, 0, 0, 0);
     }
+  }
+  // the residual values the RESID epilogue adds to, issued before the weight
+  // stream (every lane loads an in-bounds element; epilogue threads use it)
+  uint16_t hpre = 0;
+  if constexpr (EPI == GV_RESID) {
+    const int64_t nl = min(16 * (int64_t)lb + er, a.p[pi].n - 1);
+    hpre = reinterpret_cast<const uint16_t*>(a.p[pi].y)[(int64_t)min(em, M - 1) * a.p[pi].n + nl];
   }
   __builtin_amdgcn_sched_barrier(0);
   // weights and affine terms of the task, all issued before any math
@@ -156,16 +174,8 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   __builtin_amdgcn_sched_barrier(0);
 
   // epilogue operands, fetched now (they return with the weights)
-  int pi = 0;
-#pragma unroll
-  for (int q = 1; q < kGvMaxProblems; ++q)
-    if (q < a.count && rb >= a.p[q].rb0) pi = q;
-  const int lb = rb - a.p[pi].rb0;
-  const int em = threadIdx.x >> 4, er = threadIdx.x & 15;  // epilogue thread: batch row, block row
-  const bool eth = wave == 0 && em < M;
   int pos = a.pos0;
   float2 cs = make_float2(0.f, 0.f);
-  uint16_t hpre = 0;
   if constexpr (EPI == GV_ROPE) {
     if (eth && a.dpos) {
       using gint = const __attribute__((address_space(1))) int;
@@ -178,11 +188,7 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
       cs = a.dpos ? a.rope_cur[i] : a.rope_table[(int64_t)a.pos0 * (D >> 1) + i];
     }
   }
-  if constexpr (EPI == GV_RESID) {
-    const int64_t nl = 16 * (int64_t)lb + er;
-    if (eth && nl < a.p[pi].n)
-      hpre = reinterpret_cast<const uint16_t*>(a.p[pi].y)[(int64_t)em * a.p[pi].n + nl];
-  }
+
 
   // stage x in the wave's own LDS region (no barrier: only this wave reads it)
 #pragma unroll
