@@ -64,6 +64,17 @@ def q4_bytes(n, k, m=1):
     return n * k // 2 + 2 * 2 * n * (k // 64) + 2 * k * m + 2 * n * m
 
 
+def csrc_hash() -> str:
+    """sha256 over the library's kernel and host sources (name + bytes)."""
+    import hashlib
+    h = hashlib.sha256()
+    csrc = ROOT / "lokahi_amd" / "csrc"
+    for f in sorted(list(csrc.glob("*.hip")) + list(csrc.glob("*.h")) + list(csrc.glob("*.cpp"))):
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()
+
+
 def graph_time_us(fn, iters, warm=2, reps=5):
     """Duration of `fn` captured `iters` times into one HIP graph, timed with
     events around each of `reps` replays; the median replay over `iters`."""
@@ -122,14 +133,18 @@ def gemv_sets():
     xd = torch.randn((1, 14336), generator=g, device=dev).to(torch.bfloat16)
     outs = {n: torch.empty((1, sets[0][n][0].shape[0]), dtype=torch.bfloat16, device=dev)
             for n in sets[0]}
+    # the decode engine's load-time GEMV layout, one per launch group
+    lays = [{"qkv": ops.Q4Layout([W["q"], W["k"], W["v"]]),
+             "gate_up": ops.Q4Layout([W["gate"], W["up"]]),
+             "down": ops.Q4Layout([W["down"]])} for W in sets]
+    for W, L in zip(sets, lays):
+        W["_lay"] = L
     launches = [
-        ("qkv", lambda W: ops.linear_multi(x, [W["q"], W["k"], W["v"]],
-                                           outs=[outs["q"], outs["k"], outs["v"]]),
+        ("qkv", lambda W: W["_lay"]["qkv"](x, outs=[outs["q"], outs["k"], outs["v"]]),
          q4_bytes(4096, 4096) + 2 * q4_bytes(1024, 4096) - 2 * 2 * 4096),  # x read once
-        ("gate_up", lambda W: ops.linear_multi(x, [W["gate"], W["up"]],
-                                               outs=[outs["gate"], outs["up"]]),
+        ("gate_up", lambda W: W["_lay"]["gate_up"](x, outs=[outs["gate"], outs["up"]]),
          2 * q4_bytes(14336, 4096) - 2 * 4096),
-        ("down", lambda W: ops.linear_multi(xd, [W["down"]], outs=[outs["down"]]),
+        ("down", lambda W: W["_lay"]["down"](xd, outs=[outs["down"]]),
          q4_bytes(4096, 14336)),
     ]
     return sets, launches
@@ -145,13 +160,17 @@ def gemv_roofline(iters):
     tot_bytes = sum(v["bytes"] for v in per.values())
     tot_us = sum(v["avg_us"] for v in per.values())
     achieved = tot_bytes / (tot_us * 1e3)
+    # the PMC traffic figure counts only when it was measured on this build's
+    # kernel sources (profiles/q4_gemv_traffic.json records their hash)
     traffic = None
     tf = ROOT / "profiles" / "q4_gemv_traffic.json"
     if tf.exists():
-        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_set")
+        rec = json.loads(tf.read_text())
+        if rec.get("csrc_sha256") == csrc_hash():
+            traffic = rec.get("hbm_bytes_per_set")
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "q4_gemv_kernel (six-linear set, 3 launches)",
+            "kernel": "q4_gemv_mfma_kernel (six-linear set, 3 launches, GEMV layout)",
             "bytes_per_set": tot_bytes, "us_per_set": round(tot_us, 2), "launches": per}
 
 
