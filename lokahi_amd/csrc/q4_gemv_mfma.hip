@@ -105,12 +105,14 @@ constexpr int kWaveLds = MM * 2048 + 256 + MM * 64;
 template <int MP, int EPI>
 constexpr int kGvWavesPerEu = MP != 0 ? 2 : (EPI == 2 ? 4 : 7);
 
-template <int MP, int EPI, bool NORM, typename YT>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(kGvWavesPerEu<MP, EPI>)))
+// NTC: the K task count (waves per workgroup) when known at compile time
+// (4: the 8B/3B hidden width, 14: the 8B FFN width), 0 for any (up to 16).
+template <int MP, int EPI, bool NORM, typename YT, int NTC>
+__global__ __launch_bounds__(NTC ? 64 * NTC : 1024) __attribute__((amdgpu_waves_per_eu(kGvWavesPerEu<MP, EPI>)))
 void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   constexpr int MM = MP == 0 ? 1 : 4;  // staged batch rows
   extern __shared__ uint4 smem[];
-  const int nt = a.nt, M = a.M, K = a.K;
+  const int nt = NTC ? NTC : a.nt, M = a.M, K = a.K;
   const int lane = threadIdx.x & 63, j = lane >> 4, n = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rb = blockIdx.x;
@@ -121,15 +123,6 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   float* xs = reinterpret_cast<float*>(zero + 16);
   float* red = reinterpret_cast<float*>(base + nt * kWaveLds<MM>);  // [nt][MM][16]
   float* nred = red + nt * MM * 16;                                 // [nt][MM]
-
-  // the block's problem (output linear) and epilogue thread roles
-  int pi = 0;
-#pragma unroll
-  for (int q = 1; q < kGvMaxProblems; ++q)
-    if (q < a.count && rb >= a.p[q].rb0) pi = q;
-  const int lb = rb - a.p[pi].rb0;
-  const int em = threadIdx.x >> 4, er = threadIdx.x & 15;  // epilogue thread: batch row, block row
-  const bool eth = wave == 0 && em < M;
 
   // x of the task: uint4 u (0..127) = x[8u .. 8u+7] of the task, group u / 8.
   uint4 xv[MM][2], wn[2];
@@ -149,13 +142,6 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
       wn[e] = k < K ? *reinterpret_cast<const uint4*>(a.norm_w + k) : make_uint4(0, 0, 0, 0);
     }
   }
-  // the residual values the RESID epilogue adds to, issued before the weight
-  // stream (every lane loads an in-bounds element; epilogue threads use it)
-  uint16_t hpre = 0;
-  if constexpr (EPI == GV_RESID) {
-    const int64_t nl = min(16 * (int64_t)lb + er, a.p[pi].n - 1);
-    hpre = reinterpret_cast<const uint16_t*>(a.p[pi].y)[(int64_t)min(em, M - 1) * a.p[pi].n + nl];
-  }
   __builtin_amdgcn_sched_barrier(0);
   // weights and affine terms of the task, all issued before any math
   uint4 wb[8];
@@ -173,7 +159,23 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // epilogue operands, fetched now (they return with the weights)
+  // The block's problem (output linear) and the epilogue threads' roles.
+  // Looked up only now: its dependent scalar loads would otherwise hold back
+  // the weight stream.
+  int pi = 0;
+#pragma unroll
+  for (int q = 1; q < kGvMaxProblems; ++q)
+    if (q < a.count && rb >= a.p[q].rb0) pi = q;
+  const int lb = rb - a.p[pi].rb0;
+  const int em = threadIdx.x >> 4, er = threadIdx.x & 15;  // epilogue thread: batch row, block row
+  const bool eth = wave == 0 && em < M;
+  // epilogue operands, fetched now (they return with the weights); the
+  // residual values are loaded by every lane at an in-bounds index
+  uint16_t hpre = 0;
+  if constexpr (EPI == GV_RESID) {
+    const int64_t nl = min(16 * (int64_t)lb + er, a.p[pi].n - 1);
+    hpre = reinterpret_cast<const uint16_t*>(a.p[pi].y)[(int64_t)min(em, M - 1) * a.p[pi].n + nl];
+  }
   int pos = a.pos0;
   float2 cs = make_float2(0.f, 0.f);
   if constexpr (EPI == GV_ROPE) {
@@ -491,7 +493,15 @@ template <int MP, int EPI, bool NORM, typename YT>
 void launch_gv(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
   constexpr int MM = MP == 0 ? 1 : 4;
   const size_t lds = (size_t)a.nt * (kWaveLds<MM> + MM * 64 + MM * 4);
-  hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT>), dim3(nrb), dim3(64 * a.nt), lds, st,
+  if (a.nt == 4) {
+    hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 4>), dim3(nrb), dim3(256), lds, st, x, a);
+    return;
+  }
+  if (a.nt == 14 && !NORM) {
+    hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 14>), dim3(nrb), dim3(896), lds, st, x, a);
+    return;
+  }
+  hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 0>), dim3(nrb), dim3(64 * a.nt), lds, st,
                      x, a);
 }
 
