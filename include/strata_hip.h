@@ -69,13 +69,10 @@ int strata_selftest(strata_ctx* ctx, char* json, size_t cap);
  *   scales  [N, K/group] bf16, biases [N, K/group] bf16
  *   y       [M, N]   y_dtype;  y = x @ (scales*q + biases).T, fp32 accumulate
  * Rejects bits != 4, group_size != 64, K % group_size != 0 with STRATA_EINVAL
- * (mode is always "affine"). M <= 8 runs the streaming GEMV; 9 <= M < 256
- * runs the dequantize-to-LDS bf16 MFMA GEMM (bf16 x only); M >= 256 expands
- * the weight into a bf16 tile owned by ctx and multiplies it with hipBLASLt
- * (STRATA_GEMM_LT_MIN_M moves the threshold, 0 disables it).  The tile is
- * shared by the context's calls: issue large-M calls of one ctx on one
- * stream (or order the streams), and do not capture a call whose tile must
- * grow (the first call at a new largest N*K allocates). */
+ * (mode is always "affine"). M <= 8 runs the streaming GEMV; larger M
+ * (bf16 x only) runs the fused-dequant bf16 MFMA GEMMs, which re-lay the
+ * weight out into the context's scratch arena for the call: issue large-M
+ * calls of one ctx on one stream (or order the streams). */
 int strata_linear_q4(strata_ctx* ctx, const void* x, int x_dtype, int64_t M, int64_t K,
                      const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                      int64_t N, int group_size, int bits, void* y, int y_dtype,

@@ -65,7 +65,7 @@ def build(verbose: bool = False) -> Path:
             f.result()
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs),
-           f"-L{ROCM}/lib", "-lhipblaslt", f"-Wl,-rpath,{ROCM}/lib"]
+           f"-Wl,-rpath,{ROCM}/lib"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

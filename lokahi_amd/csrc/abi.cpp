@@ -105,7 +105,6 @@ int strata_ctx_destroy(strata_ctx* ctx) {
   if (!ctx) return STRATA_OK;
   hipDeviceSynchronize();
   if (ctx->scratch) hipFree(ctx->scratch);
-  strata_gemm_lt_destroy(ctx);
   delete ctx;
   return STRATA_OK;
 }

@@ -1189,9 +1189,6 @@ constexpr int kBatchedShortKeys = 2048; // batched heads: 2 per CU up to here
 constexpr int kBatchedLongKeys = 16384; // batched heads: 6 per CU from here
 void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
   int min_chunk = Lcap >= kLongSplitKeys ? 128 : 64;
-  // Overrides (timing runs) are read once per process: this runs per launch.
-  static const char* const env_min_chunk = getenv("STRATA_ATTN_MIN_CHUNK");
-  if (const char* e = env_min_chunk) min_chunk = std::max(64, atoi(e));
   // Batched heads (B*Hkv >= 64, e.g. 16 x 8): short contexts prefer longer
   // splits (1k keys: 21.6 us at 2 per CU against 24.0 at 4), very long ones
   // more of them (32k keys: 371 us at 6 against 378 at 4).  Few heads (batch
@@ -1204,7 +1201,6 @@ void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_ou
     per_cu = Lcap <= kBatchedShortKeys ? 2 : (Lcap >= kBatchedLongKeys ? 6 : 4);
   else if (Lcap >= kLongContextKeys)
     per_cu = 2;
-  if (const char* e = getenv("STRATA_ATTN_SPLITS_PER_CU")) per_cu = std::max(1, atoi(e));
   int want = (num_cus * per_cu + B * Hkv - 1) / (B * Hkv);
   if (want > kMaxDecodeSplits) want = kMaxDecodeSplits;
   int nsplit = (Lcap + min_chunk - 1) / min_chunk;
@@ -1236,8 +1232,6 @@ inline bool mfma_decode(int B, int Hkv, int64_t L) {
 constexpr int kMfmaDecodeWaves = 4;  // waves per workgroup (each with its own LDS ring)
 void decode_mfma_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
   int per_cu = 4;
-  static const char* const env_mfma_waves = getenv("STRATA_ATTN_MFMA_WAVES_PER_CU");  // once
-  if (const char* e = env_mfma_waves) per_cu = std::max(1, atoi(e));
   int ns = (num_cus * per_cu + B * Hkv - 1) / (B * Hkv);
   ns = std::max(1, std::min(ns, std::min(kMaxDecodeSplits, (Lcap + 63) / 64)));
   int chunk = (Lcap + ns - 1) / ns;
@@ -1306,13 +1300,8 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
   // chain is shorter (batch 1: 1k keys 1 head, 2k-4k keys 2 heads per
   // workgroup: 2k 8.6 -> 7.6 us, 4k 10.7 -> 10.1 us; 8k+ and batch 16 keep
   // the full group, which reads K/V once).
-  // STRATA_ATTN_HEADS_PER_WG picks a divisor of the group instead.
   int HG = G;
   while (HG % 2 == 0 && (int64_t)nsplit * B * Hkv * (G / HG) < 2 * ctx->num_cus) HG /= 2;
-  if (const char* e = getenv("STRATA_ATTN_HEADS_PER_WG")) {
-    const int h = atoi(e);
-    if (h > 0 && G % h == 0 && (h == 1 || h == 2 || h == 3 || h == 4 || h == 6 || h == 8)) HG = h;
-  }
   dim3 grid(nsplit, Hkv * (G / HG), B);
 #define STRATA_DEC(GV)                                                                        \
   if (HG == GV)                                                                               \

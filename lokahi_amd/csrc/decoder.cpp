@@ -60,7 +60,7 @@ struct strata_decoder {
   float graph_temp;
   // Prefill GEMM layout of each layer's launches (q/k/v, o, gate/up, down),
   // re-laid out once at creation (null: re-laid out per call).
-  std::vector<void*> packed;
+  std::vector<GemmPacked> packed;
   // Decode GEMV layout of the same launches (4 per layer, q4_gemv_mfma.hip),
   // built once at creation; empty when the model's shapes do not fit it
   // (the decode step then runs the MLX-layout GEMV).
@@ -180,8 +180,8 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
     qkv[2].y = d->v;
     void* kc = kv->kl(li);
     void* vc = kv->vl(li);
-    const void* const* pk = d->packed.empty() ? nullptr : &d->packed[(size_t)li * 4];
-    RC(strata_q4_gemm_multi(d->ctx, d->xn, T, H, qkv, 3, STRATA_BF16, stream, pk ? pk[0] : nullptr));
+    const GemmPacked* pk = d->packed.empty() ? nullptr : &d->packed[(size_t)li * 4];
+    RC(strata_q4_gemm_multi(d->ctx, d->xn, T, H, qkv, 3, STRATA_BF16, stream, pk ? &pk[0] : nullptr));
     RC(strata_rope_kv_fused_launch(d->q, d->k, d->v, STRATA_BF16, B, Hq, Hkv, L, D, kv->Lmax,
                                    pos0, nullptr, c.rope_theta, d->qr, kc, vc, STRATA_BF16,
                                    stream));
@@ -193,17 +193,17 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
     strata_q4_weight o = Lw.o;
     o.y = d->o;
     RC(strata_q4_gemm_multi(d->ctx, d->attn, T, Hq * D, &o, 1, STRATA_BF16, stream,
-                            pk ? pk[1] : nullptr));
+                            pk ? &pk[1] : nullptr));
     RC(strata_rmsnorm_launch(d->h, d->o, Lw.post_norm, T, H, c.rms_norm_eps, d->xn, stream));
     strata_q4_weight gu[2] = {Lw.gate, Lw.up};
     gu[0].y = d->gate;
     gu[1].y = d->up;
-    RC(strata_q4_gemm_multi(d->ctx, d->xn, T, H, gu, 2, STRATA_BF16, stream, pk ? pk[2] : nullptr));
+    RC(strata_q4_gemm_multi(d->ctx, d->xn, T, H, gu, 2, STRATA_BF16, stream, pk ? &pk[2] : nullptr));
     RC(strata_silu_mul_launch(d->gate, d->up, (int64_t)T * F, d->act, stream));
     strata_q4_weight dn = Lw.down;
     dn.y = d->delta;
     RC(strata_q4_gemm_multi(d->ctx, d->act, T, F, &dn, 1, STRATA_BF16, stream,
-                            pk ? pk[3] : nullptr));
+                            pk ? &pk[3] : nullptr));
   }
   // final norm of h + delta, then lm_head on the last position of each row
   RC(strata_rmsnorm_launch(d->h, d->delta, d->final_norm, T, H, c.rms_norm_eps, d->hn, stream));
@@ -254,7 +254,10 @@ int pack_prefill_weights(strata_decoder* d) {
   static const bool skip = getenv("STRATA_DECODER_NO_PREFILL_PACK") != nullptr;
   if (skip || d->max_tokens < kMfmaMidRows) return STRATA_OK;
   const int H = c.hidden_size, F = c.intermediate_size, QW = c.num_heads * c.head_dim;
-  std::vector<void*> packed;
+  std::vector<GemmPacked> packed;
+  auto drop = [&]() {
+    for (GemmPacked& q : packed) (void)hipFree(const_cast<void*>(q.buf));
+  };
   for (const strata_llama_layer& L : d->layers) {
     const strata_q4_weight groups[4][3] = {{L.q, L.k, L.v}, {L.o}, {L.gate, L.up}, {L.down}};
     const int counts[4] = {3, 1, 2, 1}, Ks[4] = {H, QW, H, F};
@@ -263,7 +266,7 @@ int pack_prefill_weights(strata_decoder* d) {
       for (int i = 0; i < counts[gi]; ++i) {
         const strata_q4_weight& w = groups[gi][i];
         if (w.N % 256 != 0 || !aligned16(w.w)) {
-          for (void* p : packed) hipFree(p);
+          drop();
           return STRATA_OK;  // this model's prefill re-lays out per call
         }
         N += w.N;
@@ -271,13 +274,18 @@ int pack_prefill_weights(strata_decoder* d) {
       void* p = nullptr;
       if (hipMalloc(&p, strata_q4_gemm_mfma_scratch(N, Ks[gi])) != hipSuccess) {
         (void)hipGetLastError();
-        for (void* q : packed) hipFree(q);
+        drop();
         return STRATA_OK;
       }
-      packed.push_back(p);
+      GemmPacked g;
+      g.buf = p;
+      g.N = N;
+      g.K = Ks[gi];
+      g.count = counts[gi];
+      packed.push_back(g);
       const int rc = strata_q4_gemm_pack(groups[gi], counts[gi], Ks[gi], p, nullptr);
       if (rc) {
-        for (void* q : packed) hipFree(q);
+        drop();
         return rc;
       }
     }
@@ -400,7 +408,7 @@ int strata_decoder_destroy(strata_decoder* d) {
   if (!d) return STRATA_OK;
   hipDeviceSynchronize();
   for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
-  for (void* p : d->packed) hipFree(p);
+  for (GemmPacked& p : d->packed) (void)hipFree(const_cast<void*>(p.buf));
   for (GemvLayout& L : d->dlay) strata_gemv_layout_free(&L);
   strata_gemv_layout_free(&d->head_lay);
   void* ptrs[] = {d->h, d->xn, d->q, d->k, d->v, d->qr, d->attn, d->o, d->gate, d->up, d->act,

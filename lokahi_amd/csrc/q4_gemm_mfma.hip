@@ -541,7 +541,6 @@ int splitk_slices(int M, int K, int N, int cus) {
   int p2 = 1;
   while (p2 * 2 <= S) p2 *= 2;
   S = p2;
-  if (const char* e = getenv("STRATA_GEMM_SPLITK")) S = atoi(e);
   S = std::min(S, std::min(G >= 128 ? 16 : 8, std::max(1, G / 4)));
   return std::max(S, 1);
 }
@@ -625,7 +624,6 @@ int strata_q4_gemm_mfma_run(const void* x, int M, int K, const void* packed,
   // tiles unless that leaves the GPU under two workgroups per CU.
   auto go = [&](int ntile0, int nts, int S) {
     bool big = S == 1 && (int64_t)((M + 255) / 256) * nts >= 2 * cus;
-    if (const char* e = getenv("STRATA_GEMM_TM")) big = S == 1 && atoi(e) == 256;  // timing runs
     const int TM = big ? 256 : 128;
     const GemmSplit sp{(M + TM - 1) / TM, ntile0, nts, S, S > 1 ? part : nullptr};
     if (S > 1)  // 128-row tiles; the partial sums are fp32 whatever y's dtype

@@ -769,19 +769,10 @@ GemvShape pick_shape(int nv, int rows, int M) {
     g.r = 1;
     g.u = 4;
   }
-  // Geometry overrides (timing runs), read once per process: this runs for
-  // every decode launch.
-  static const char* const env_nw = getenv("STRATA_GEMV_NW");
-  static const char* const env_r = getenv("STRATA_GEMV_R");
-  static const char* const env_u = getenv("STRATA_GEMV_U");
-  if (env_nw) g.nw = atoi(env_nw);
-  if (env_r) g.r = atoi(env_r);
-  if (env_u) g.u = atoi(env_u);
   return g;
 }
 
-// Persistent grid size: workgroups per CU times CUs (STRATA_GEMV_WGS_PER_CU
-// overrides the per-CU count).  8-wave launches (small or long-row linears)
+// Persistent grid size: workgroups per CU times CUs.  8-wave launches (small or long-row linears)
 // get one row block per workgroup at the decode shapes; U >= 7 (batched
 // long rows) runs three 4-wave workgroups per CU over several row blocks.
 int g_num_cus = 256;
@@ -789,12 +780,8 @@ int g_num_cus = 256;
 // for 5 waves per SIMD).
 int grid_cap(int nw, int u, bool norm, bool five_waves) {
   int per_cu = u >= 7 ? 3 : (nw >= 8 ? 6 : (five_waves ? 5 : 4));
-  static const char* const env_wgs = getenv("STRATA_GEMV_WGS_PER_CU");  // read once
-  if (env_wgs) per_cu = atoi(env_wgs);
   if (norm) {  // each workgroup normalizes x itself: 5 per CU measured best
     per_cu = 5;  // (with the prologue at raised wave priority; 4 before it)
-    static const char* const env_nwgs = getenv("STRATA_GEMV_NORM_WGS_PER_CU");
-    if (env_nwgs) per_cu = atoi(env_nwgs);
   }
   return std::max(1, per_cu) * g_num_cus;
 }

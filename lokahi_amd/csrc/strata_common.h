@@ -194,7 +194,6 @@ struct strata_ctx {
   int max_lds_per_block;
   void* scratch;        // device scratch arena (split-K partials), grown on demand
   size_t scratch_bytes;
-  struct GemmLt* lt;    // prefill GEMM state (library handle, plans, bf16 weight tile)
   float* fixed_scratch; // this device's copy of the library's static scratch array
 };
 

@@ -61,12 +61,10 @@ int strata_bf16_gemv(strata_ctx* ctx, const void* x, int M, int K, const uint16_
 int strata_q4_gemm_launch(const void* x, int M, int K, const uint32_t* w, const uint16_t* s,
                           const uint16_t* b, int N, void* y, int y_dtype, void* stream);
 // Prefill q4 linear (bf16 x, M > 8): the hand-written fused-dequant MFMA
-// kernels; STRATA_GEMM_LT_MIN_M > 0 opts into dequantize + hipBLASLt from
-// that many rows.
+// kernels.
 int strata_q4_gemm(strata_ctx* ctx, const void* x, int M, int K, const uint32_t* w,
                    const uint16_t* s, const uint16_t* b, int N, void* y, int y_dtype,
                    void* stream);
-void strata_gemm_lt_destroy(strata_ctx* ctx);
 // 256-column-tile fused-dequant MFMA GEMM (M >= kMfmaMidRows on the default
 // path).
 // scratch: strata_q4_gemm_mfma_scratch(N, K) bytes, 16-byte aligned (the
@@ -96,8 +94,16 @@ size_t strata_q4_gemm_mfma_part_bytes(int M, int K, const strata_q4_weight* ws, 
 constexpr int kMfmaMidRows = 40;
 // Prefill linears sharing x (M > 8 rows, bf16 x): one launch where the
 // shapes allow, else one per linear.
+// A load-time re-layout (strata_q4_gemm_pack) of `count` linears with N
+// rows in all and width K; a call uses it only when it matches.
+struct GemmPacked {
+  const void* buf = nullptr;
+  int64_t N = 0;
+  int K = 0;
+  int count = 0;
+};
 int strata_q4_gemm_multi(strata_ctx* ctx, const void* x, int M, int K, const strata_q4_weight* ws,
-                         int count, int y_dtype, void* stream, const void* packed = nullptr);
+                         int count, int y_dtype, void* stream, const GemmPacked* packed = nullptr);
 // Linears sharing x for a few rows (M <= kSkinnyMaxRows, K % 512 == 0, every
 // N % 16 == 0, 16-byte aligned weights and x): one launch, each weight read once.
 constexpr int kSkinnyMaxRows = 64;

@@ -36,23 +36,6 @@ def test_config5_attention_8k_rows_match_oracle_and_decode(dev):
             assert rel_err(got, ref) < TOL_BF16, row
 
 
-def test_config5_gate_gemm_8k_library_and_fused_paths(dev, monkeypatch):
-    from lokahi_amd import ops
-    M, N, K = 8192, 14336, 4096
-    rng = np.random.default_rng(14336)
-    w, s, b = q4.quantize(rng.normal(0, 0.02, (N, K)).astype(np.float32), 64)
-    x = f32_to_bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
-    tw, ts, tb, tx = (to_dev(a, dev) for a in (w, s, b, x))
-    monkeypatch.setenv("STRATA_GEMM_LT_MIN_M", "256")
-    lib = ops.linear(tx, tw, ts, tb, out_dtype=torch.float32)
-    monkeypatch.setenv("STRATA_GEMM_LT_MIN_M", "0")
-    fused = ops.linear(tx, tw, ts, tb, out_dtype=torch.float32)
-    assert rel_err(to_np_f32(lib), to_np_f32(fused)) < TOL_F32
-    rows = np.array([0, 1, 255, 256, 4097, 8191])
-    ref = q4.quantized_matmul(bf16_bits_to_f32(x[rows]), w, s, b)
-    assert rel_err(to_np_f32(lib)[rows], ref) < TOL_BF16
-
-
 @pytest.mark.parametrize("name,N,K", [("q/o", 4096, 4096), ("k/v", 1024, 4096),
                                       ("up", 14336, 4096), ("down", 4096, 14336)])
 def test_config5_layer_gemms_8k_sampled_rows(dev, name, N, K):

@@ -101,25 +101,21 @@ def test_gemm_prefill_matches_oracle(dev, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 1024), (512, 4096, 4096), (257, 96, 64)])
-def test_gemm_library_path_and_fused_kernel_agree(dev, monkeypatch, M, N, K):
-    """Prefill rows >= STRATA_GEMM_LT_MIN_M take dequant + hipBLASLt; fewer take
-    the fused-dequant MFMA kernel.  Both multiply the same bf16 weight values."""
+def test_gemm_prefill_rows_match_oracle(dev, M, N, K):
+    """Prefill rows run the fused-dequant kernels (MFMA, or the 128 x 128 tile
+    kernel for N not a multiple of 256): the bf16-staged product within fp32
+    tolerance, the exact product within bf16 tolerance."""
     from lokahi_amd import ops
     rng = np.random.default_rng(M + N + K)
     w, s, b, x = _problem(rng, N, K, M)
-    args = [to_dev(x, dev)] + [to_dev(a, dev) for a in (w, s, b)]
+    tw, ts, tb = (to_dev(a, dev) for a in (w, s, b))
     ref = q4.quantized_matmul(bf16_bits_to_f32(x), w, s, b)
     wq = round_bf16(q4.dequantize(w, s, b, 64).astype(np.float32)).astype(np.float64)
     ref_b = bf16_bits_to_f32(x).astype(np.float64) @ wq.T
-    outs = {}
-    for path, min_m in (("library", "1"), ("fused", "0")):
-        monkeypatch.setenv("STRATA_GEMM_LT_MIN_M", min_m)
-        y32 = to_np_f32(ops.linear(*args, out_dtype=torch.float32))
-        y16 = to_np_f32(ops.linear(*args))
-        assert rel_err(y32, ref_b) < TOL_F32, path
-        assert rel_err(y16, ref) < TOL_BF16, path
-        outs[path] = y32
-    assert rel_err(outs["library"], outs["fused"]) < TOL_F32
+    y32 = to_np_f32(ops.linear(to_dev(x, dev), tw, ts, tb, out_dtype=torch.float32))
+    y16 = to_np_f32(ops.linear(to_dev(x, dev), tw, ts, tb))
+    assert rel_err(y32, ref_b) < TOL_F32
+    assert rel_err(y16, ref) < TOL_BF16
 
 
 def test_linear_rejects_bad_parameters(dev):
@@ -158,21 +154,19 @@ def test_quantizer_is_bit_exact_with_oracle(dev):
     assert np.array_equal(bi.cpu().view(torch.int16).numpy().view(np.uint16), eb)
 
 
-def test_gemm_library_plan_cache_survives_many_prompt_lengths(dev, monkeypatch):
-    """Prefill M is the prompt length: more distinct lengths than the plan
-    cache holds (256) must keep giving correct results across the eviction."""
+def test_gemm_many_prompt_lengths(dev):
+    """Prefill M is the prompt length: a run of distinct lengths through the
+    per-call re-layout and split-K routing stays correct."""
     from lokahi_amd import ops
-    monkeypatch.setenv("STRATA_GEMM_LT_MIN_M", "1")
     rng = np.random.default_rng(260)
-    N, K = 64, 128
+    N, K = 256, 128
     w, s, b, x = _problem(rng, N, K, 600)
     tw, ts, tb, tx = (to_dev(a, dev) for a in (w, s, b, x))
     wq = round_bf16(q4.dequantize(w, s, b, 64).astype(np.float32)).astype(np.float64)
-    for M in range(300, 560):
+    for M in range(300, 560, 7):
         y = ops.linear(tx[:M], tw, ts, tb, out_dtype=torch.float32)
-        if M in (300, 301, 555, 559):
-            ref = bf16_bits_to_f32(x[:M]).astype(np.float64) @ wq.T
-            assert rel_err(to_np_f32(y), ref) < TOL_F32, M
+        ref = bf16_bits_to_f32(x[:M]).astype(np.float64) @ wq.T
+        assert rel_err(to_np_f32(y), ref) < TOL_F32, M
 
 
 @pytest.mark.parametrize("M,K", [(9, 1024), (16, 3584), (17, 1024), (40, 2048), (64, 1024),

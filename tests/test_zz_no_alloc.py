@@ -41,16 +41,14 @@ def test_noalloc_attention_matches_allocating_entry_point(dev, dtype):
 def test_noalloc_attention_rejects_oversized_scratch_and_bad_shapes(dev, monkeypatch):
     from lokahi_amd import _abi
     lib = _abi.load()
-    # 64 splits per CU: 16 x 64 query heads over 16k keys then need 128 splits,
-    # 69 MB of partials, more than the static scratch holds: rejected before
-    # any launch
-    monkeypatch.setenv("STRATA_ATTN_SPLITS_PER_CU", "64")
-    q = torch.zeros((16, 64, 1, 128), device=dev, dtype=torch.bfloat16)
-    k = torch.zeros((16, 8, 16384, 128), device=dev, dtype=torch.bfloat16)
+    # one KV head with 128 query heads over 32k keys: 256 key splits, 17 MB
+    # of partials, more than the static scratch holds: rejected before any
+    # launch
+    q = torch.zeros((1, 128, 1, 128), device=dev, dtype=torch.bfloat16)
+    k = torch.zeros((1, 1, 32768, 128), device=dev, dtype=torch.bfloat16)
     out = torch.empty_like(q)
     rc = _call(lib.strata_attn_gqa_noalloc, q, k, k, out)
     assert rc == _abi.STRATA_EINVAL and "static scratch" in _abi.last_error()
-    monkeypatch.delenv("STRATA_ATTN_SPLITS_PER_CU")
     q3 = torch.zeros((1, 6, 1, 128), device=dev)
     k3 = torch.zeros((1, 4, 8, 128), device=dev)
     rc = _call(lib.strata_attn_gqa_noalloc, q3, k3, k3, torch.empty_like(q3))
