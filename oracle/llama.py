@@ -218,3 +218,41 @@ def flatten_names(cfg: Config) -> List[str]:
         for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
             names += [p + n + ".weight", p + n + ".scales", p + n + ".biases"]
     return names
+
+
+def random_q4_weights(cfg: Config, seed: int, scale: float = 0.0067) -> Dict[str, np.ndarray]:
+    """Seeded full-size weights drawn directly in the q4 format (test helper).
+
+    Codes are uniform 0..15; per group ``s = scale * (1 + 0.1 n1)`` and
+    ``b = -7.5 s (1 + 0.05 n2)`` (bf16), which gives weights of std ~0.03
+    centred near 0, as a group-64 quantization of N(0, 0.02) would; embedding
+    and lm_head are N(0, 0.02) bf16 (truncated draws), norms ones.  Skips ``quantize`` so that a
+    28-layer 3B model is drawn in seconds."""
+    rng = np.random.default_rng(seed)
+    hs, fs = cfg.hidden_size, cfg.intermediate_size
+    hq, hkv, d, g = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.group_size
+    shapes = {"q_proj": (hq * d, hs), "k_proj": (hkv * d, hs), "v_proj": (hkv * d, hs),
+              "o_proj": (hs, hq * d), "gate_proj": (fs, hs), "up_proj": (fs, hs),
+              "down_proj": (hs, fs)}
+
+    def bf16(x):  # truncation: any bit pattern is a valid draw, and it is fast
+        return (np.ascontiguousarray(x, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+    def normal(shape, std):
+        return bf16(rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+
+    w: Dict[str, np.ndarray] = {"embed_tokens": normal((cfg.vocab_size, hs), 0.02)}
+    ones = bf16(np.ones(hs, dtype=np.float32))
+    for li in range(cfg.num_hidden_layers):
+        p = f"layers.{li}."
+        for name, (n, k) in shapes.items():
+            s = np.float32(scale) * (1 + np.float32(0.1) * rng.standard_normal((n, k // g), dtype=np.float32))
+            b = np.float32(-7.5) * s * (1 + np.float32(0.05) * rng.standard_normal((n, k // g), dtype=np.float32))
+            w[p + name + ".weight"] = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint32)
+            w[p + name + ".scales"] = bf16(s)
+            w[p + name + ".biases"] = bf16(b)
+        w[p + "input_layernorm"] = ones
+        w[p + "post_attention_layernorm"] = ones
+    w["norm"] = ones
+    w["lm_head"] = normal((cfg.vocab_size, hs), 0.02)
+    return w
