@@ -66,6 +66,13 @@ typedef struct {
   const uint16_t* const* b;
 } OracleLlama;
 
+/* Accumulation-order probe: when set, the linears accumulate in fp32 (group
+ * sums, then a running fp32 total) instead of double.  The greedy ids of a
+ * test model that change under this switch depend on accumulation order, so
+ * they cannot be compared bit-exactly against any fp32 implementation. */
+static int g_f32_accum = 0;
+void oracle_llama_set_f32_accum(int on) { g_f32_accum = on != 0; }
+
 /* y[m, n] = fp32(sum_k x[m, k] * (s*q + b)[n, k]) in double; x holds bf16 values. */
 static void linear(const float* x, int M, int K, const uint32_t* w, const uint16_t* s,
                    const uint16_t* b, int N, int G, float* y) {
@@ -86,6 +93,16 @@ static void linear(const float* x, int M, int K, const uint32_t* w, const uint16
       }
       for (int m = 0; m < M; ++m) {
         const double* xr = xd + (int64_t)m * K;
+        if (g_f32_accum) { /* perturbed variant: fp32 group sums, fp32 total */
+          float acc = 0.f;
+          for (int g = 0; g < ng; ++g) {
+            float p = 0.f;
+            for (int k = g * G; k < (g + 1) * G; ++k) p += (float)xr[k] * (float)wr[k];
+            acc += p;
+          }
+          y[(int64_t)m * N + n] = acc;
+          continue;
+        }
         double a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         for (int k = 0; k < K; k += 8)
           for (int j = 0; j < 8; ++j) a[j] += xr[k + j] * wr[k + j];

@@ -220,7 +220,8 @@ def flatten_names(cfg: Config) -> List[str]:
     return names
 
 
-def random_q4_weights(cfg: Config, seed: int, scale: float = 0.0067) -> Dict[str, np.ndarray]:
+def random_q4_weights(cfg: Config, seed: int, scale: float = 0.0067,
+                      embed_std: float = 0.02) -> Dict[str, np.ndarray]:
     """Seeded full-size weights drawn directly in the q4 format (test helper).
 
     Codes are uniform 0..15; per group ``s = scale * (1 + 0.1 n1)`` and
@@ -241,7 +242,7 @@ def random_q4_weights(cfg: Config, seed: int, scale: float = 0.0067) -> Dict[str
     def normal(shape, std):
         return bf16(rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
 
-    w: Dict[str, np.ndarray] = {"embed_tokens": normal((cfg.vocab_size, hs), 0.02)}
+    w: Dict[str, np.ndarray] = {"embed_tokens": normal((cfg.vocab_size, hs), embed_std)}
     ones = bf16(np.ones(hs, dtype=np.float32))
     for li in range(cfg.num_hidden_layers):
         p = f"layers.{li}."

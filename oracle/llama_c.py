@@ -38,6 +38,7 @@ def _lib():
     lib = C.CDLL(str(_SO))
     lib.oracle_llama_generate.argtypes = [C.POINTER(_Model), _P, C.c_int, C.c_int, _P, _P, _P]
     lib.oracle_llama_generate.restype = C.c_int
+    lib.oracle_llama_set_f32_accum.argtypes = [C.c_int]
     return lib
 
 
@@ -73,6 +74,11 @@ class CLlama:
                          arr("lm_head", np.uint16) if "lm_head" in weights else None,
                          ln1, ln2, ws, ss, bs)
         self._lib = _lib()
+
+    def set_f32_accum(self, on: bool) -> None:
+        """Switch the linears to fp32 accumulation (an accumulation-order probe:
+        ids that change under it are ill-conditioned for bit-exact checks)."""
+        self._lib.oracle_llama_set_f32_accum(1 if on else 0)
 
     def generate(self, prompt, max_new_tokens: int) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
         """Greedy ids ``[n_prompt + max_new]``, per-token top-1/top-2 logit

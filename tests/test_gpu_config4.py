@@ -5,9 +5,11 @@ native engine (greedy loop of ``generation.py:7-50`` over
 
 * a 2-layer model of that geometry: greedy token ids bit-exact against the
   NumPy oracle;
-* the full 28-layer model with a 64-token prompt and 16 greedy tokens: ids
+* the full 28-layer model with 64-token prompts and 16 greedy tokens: ids
   bit-exact against the C decoder oracle (``oracle/c/strata_oracle_llama.c``,
-  pinned against the NumPy oracle in ``tests/test_oracle_llama_c.py``);
+  pinned against the NumPy oracle in ``tests/test_oracle_llama_c.py``) in a
+  well-conditioned weight draw, and prefill logits within the oracle's own
+  accumulation-order noise in the default (chaotic) draw;
 * the full 28-layer model with the 2048-token prompt and 256 greedy tokens:
   graph-replayed steps give the same ids as host-launched steps, and the
   engine's logits match the op-by-op driver's.
@@ -69,32 +71,75 @@ def test_config4_full_28_layers_prompt_2048_plus_256_tokens(dev):
         assert rel_err(a, b) < 2e-2, n
 
 
-# weights seed 2026, prompt seed 2: the C oracle's smallest top-1/top-2 logit
-# gap over the 16 greedy steps is 0.061, so the argmax at every step is far
-# from a tie relative to fp32-vs-float64 accumulation differences
-FULL_W_SEED, FULL_PROMPT_SEED, MIN_MARGIN = 2026, 2, 0.01
-FULL_C_IDS = [111333, 116464, 64043, 34930, 111568, 15028, 30922, 2482, 99915, 65606, 11264,
-              37124, 74479, 35015, 113684, 112227]
+
+# Full depth against the C oracle.  A 28-layer random-init model is a chaotic
+# map: with the default draw (q4 scale 0.0067, embedding std 0.02) merely
+# switching the oracle's own linears from double to fp32 accumulation moves
+# the prefill logits by ~0.3 (of ~5) and changes the greedy ids within a few
+# tokens, so no fp32 implementation can match its ids bit for bit.  With a
+# smaller q4 scale and a unit-std embedding the residual stream is better
+# conditioned (the fp32 probe moves the logits by ~0.02 and leaves all 16 ids
+# unchanged; the layers still change 14 and 16 of the 16 ids of the two prompts
+# below against a 0-layer model): there the ids must be bit-exact.  In the chaotic draw the engine's
+# logits must stay within a small multiple of the probe's own change.
+W_SEED = 2026
+WELL = dict(scale=0.001, embed_std=1.0)
+
+
+def _c_oracle(ocfg, hw):
+    from oracle import llama_c
+    return llama_c.CLlama(ocfg, hw)
+
+
+def _full_model(hw):
+    from lokahi_amd.llama import DecoderEngine, HipLlamaForCausalLM, weights_to_device
+    model = HipLlamaForCausalLM(_cfg(28), weights_to_device(hw))
+    cache = model.new_cache(1, 96)
+    return model, cache, DecoderEngine(model, cache, max_batch=1, max_tokens=96)
+
+
+def _prefill_logits(eng, cache, ids):
+    cache.clear()
+    return to_np_f32(eng.forward(torch.from_numpy(ids))).reshape(-1)
 
 
 def test_config4_full_28_layers_tokens_bit_exact_vs_c_oracle(dev):
-    from lokahi_amd.llama import HipLlamaForCausalLM, weights_to_device
-    from oracle import llama_c
     ocfg = oll.Config(128256, 3072, 8192, 28, 24, 8)
-    hw = oll.random_q4_weights(ocfg, FULL_W_SEED)
-    prompt = np.random.default_rng(FULL_PROMPT_SEED).integers(0, ocfg.vocab_size, (1, 64))
-    ids, margins, last_logits = llama_c.CLlama(ocfg, hw).generate(prompt, 16)
-    assert margins.min() >= MIN_MARGIN, margins
-    assert ids[64:].tolist() == FULL_C_IDS
+    hw = oll.random_q4_weights(ocfg, W_SEED, **WELL)
+    cm = _c_oracle(ocfg, hw)
+    model, cache, eng = _full_model(hw)
+    for ps in (3, 7):
+        prompt = np.random.default_rng(ps).integers(0, ocfg.vocab_size, (1, 64))
+        ids, margins, _ = cm.generate(prompt, 16)
+        assert margins.min() >= 0.02, (ps, margins)  # no near-tie among the 16 argmaxes
+        cache.clear()
+        got = eng.generate(torch.from_numpy(prompt), 16).cpu().numpy()[0]
+        assert np.array_equal(got, ids), f"prompt seed {ps}\n{got[64:]}\n{ids[64:]}"
+        _, _, lg = cm.generate(prompt, 1)
+        cm.set_f32_accum(True)
+        try:
+            _, _, lg32 = cm.generate(prompt, 1)
+        finally:
+            cm.set_f32_accum(False)
+        probe = np.abs(lg32 - lg).max()
+        gpu = np.abs(_prefill_logits(eng, cache, prompt) - lg).max()
+        assert gpu <= 2.0 * probe + 1e-3, (ps, gpu, probe)
 
-    model = HipLlamaForCausalLM(_cfg(28), weights_to_device(hw))
+
+def test_config4_full_28_layers_chaotic_draw_within_accumulation_noise(dev):
+    ocfg = oll.Config(128256, 3072, 8192, 28, 24, 8)
+    hw = oll.random_q4_weights(ocfg, W_SEED)
+    cm = _c_oracle(ocfg, hw)
+    prompt = np.random.default_rng(2).integers(0, ocfg.vocab_size, (1, 64))
+    ids, margins, lg = cm.generate(prompt, 1)
+    cm.set_f32_accum(True)
+    try:
+        _, _, lg32 = cm.generate(prompt, 1)
+    finally:
+        cm.set_f32_accum(False)
+    probe = np.abs(lg32 - lg).max()
+    model, cache, eng = _full_model(hw)
     del hw
-    got = model.generate(torch.from_numpy(prompt), max_new_tokens=16).cpu().numpy()
-    assert np.array_equal(got[0], ids), f"\n{got[0, 64:]}\n{ids[64:]}"
-    # the logits that chose the last token, through the engine's prefill path
-    cache = model.new_cache(1, 96)
-    from lokahi_amd.llama import DecoderEngine
-    eng = DecoderEngine(model, cache, max_batch=1, max_tokens=96)
-    lg = to_np_f32(eng.forward(torch.from_numpy(ids[None, :-1])))
-    assert rel_err(lg.reshape(-1), last_logits) < 2e-2
-    assert int(np.argmax(lg.reshape(-1))) == ids[-1]
+    g = _prefill_logits(eng, cache, prompt)
+    gpu = np.abs(g - lg).max()
+    assert gpu <= 3.0 * probe, (gpu, probe)
