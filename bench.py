@@ -244,7 +244,7 @@ def attention_decode():
     from lokahi_amd import ops
     dev = torch.device("cuda", 0)
     res = []
-    for B, L in [(1, 1024), (1, 8192), (1, 32768), (16, 1024), (16, 8192), (16, 32768)]:
+    for B, L in [(1, 1024), (1, 2048), (1, 8192), (1, 32768), (16, 1024), (16, 8192), (16, 32768)]:
         g = torch.Generator(device=dev).manual_seed(B * 7 + L)
         q = torch.randn((B, 32, 1, 128), generator=g, device=dev).to(torch.bfloat16)
         k = torch.randn((B, 8, L + 1, 128), generator=g, device=dev).to(torch.bfloat16)

@@ -237,3 +237,41 @@ def test_decode_batched_heads_mfma(dev, B, Hq, Hkv, D, L):
     ref = att.naive_gqa(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64), pos)
     assert rel_err(out, ref) < TOL_BF16
     assert np.abs(out - ref).max() < 2e-2
+
+
+def test_decode_split_k_back_to_back_and_graph_replays(dev):
+    """Split-K decode calls of different geometry in a row (the partials of
+    one call in the scratch arena the next call reuses), then graph replays of
+    one call with eager calls of another geometry in between: every output
+    must match the float64 attention."""
+    from lokahi_amd import ops
+    rng = np.random.default_rng(2048)
+    cases = [(1, 32, 8, 128, 2049), (1, 24, 8, 128, 777), (2, 8, 8, 64, 300),
+             (1, 32, 8, 128, 4100), (1, 8, 1, 128, 1500), (1, 32, 8, 128, 65)]
+    data = []
+    for B, Hq, Hkv, D, L in cases:
+        q = round_bf16(rng.normal(size=(B, Hq, 1, D)).astype(np.float32))
+        k = round_bf16(rng.normal(size=(B, Hkv, L, D)).astype(np.float32))
+        v = round_bf16(rng.normal(size=(B, Hkv, L, D)).astype(np.float32))
+        ref = att.naive_gqa(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64))
+        data.append(([bf16_dev(a, dev) for a in (q, k, v)], ref))
+    for rep in range(2):
+        for (tq, tk, tv), ref in data:
+            out = to_np_f32(ops.attention(tq, tk, tv))
+            assert rel_err(out, ref) < TOL_BF16 and np.abs(out - ref).max() < 2e-2, rep
+    (tq, tk, tv), ref = data[0]
+    out = torch.empty_like(tq)
+    ops.attention(tq, tk, tv, out=out)  # eager first: sizes the scratch arena
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.attention(tq, tk, tv, out=out)
+    (eq, ek, ev), eref = data[1]
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        got = to_np_f32(out)
+        assert rel_err(got, ref) < TOL_BF16 and np.abs(got - ref).max() < 2e-2
+        e = to_np_f32(ops.attention(eq, ek, ev))
+        assert rel_err(e, eref) < TOL_BF16
