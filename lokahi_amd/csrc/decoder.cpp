@@ -247,12 +247,12 @@ void set_lengths(strata_decoder* d, int len) {
 // prefill, in the layout of q4_gemm_relayout_kernel, when prefills can reach
 // the 256-column MFMA kernel and every linear qualifies.  Costs one more copy of the
 // q4 linears; on an allocation failure the prefill re-lays out per call.
-// STRATA_DECODER_NO_PREFILL_PACK (read once) skips it: prefills then
-// re-lay out per call and the copy's memory is not held.
+// STRATA_DECODER_NO_PREFILL_PACK (read per decoder creation) skips it:
+// prefills then re-lay out per call and the copy's memory is not held.
 int pack_prefill_weights(strata_decoder* d) {
   const strata_llama_config& c = d->cfg;
-  static const bool skip = getenv("STRATA_DECODER_NO_PREFILL_PACK") != nullptr;
-  if (skip || d->max_tokens < kMfmaMidRows) return STRATA_OK;
+  if (getenv("STRATA_DECODER_NO_PREFILL_PACK") != nullptr || d->max_tokens < kMfmaMidRows)
+    return STRATA_OK;
   const int H = c.hidden_size, F = c.intermediate_size, QW = c.num_heads * c.head_dim;
   std::vector<GemmPacked> packed;
   auto drop = [&]() {
