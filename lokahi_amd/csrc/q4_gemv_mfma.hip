@@ -106,7 +106,8 @@ template <int MP, int EPI>
 constexpr int kGvWavesPerEu = MP != 0 ? 2 : (EPI == 2 ? 4 : 7);
 
 // NTC: the K task count (waves per workgroup) when known at compile time
-// (4: the 8B/3B hidden width, 14: the 8B FFN width), 0 for any (up to 16).
+// (4: the 8B hidden width, 14: the 8B FFN width, 3 and 8: the 3B widths),
+// 0 for any (up to 16).
 template <int MP, int EPI, bool NORM, typename YT, int NTC>
 __global__ __launch_bounds__(NTC ? 64 * NTC : 1024) __attribute__((amdgpu_waves_per_eu(kGvWavesPerEu<MP, EPI>)))
 void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
@@ -500,6 +501,16 @@ void launch_gv(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
   if (a.nt == 14 && !NORM) {
     hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 14>), dim3(nrb), dim3(896), lds, st, x, a);
     return;
+  }
+  if constexpr (MP == 0) {  // batch 1 at the 3B widths (3072, and 8192 for down)
+    if (a.nt == 3) {
+      hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 3>), dim3(nrb), dim3(192), lds, st, x, a);
+      return;
+    }
+    if (a.nt == 8 && !NORM) {
+      hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 8>), dim3(nrb), dim3(512), lds, st, x, a);
+      return;
+    }
   }
   hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 0>), dim3(nrb), dim3(64 * a.nt), lds, st,
                      x, a);
