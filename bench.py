@@ -56,7 +56,7 @@ def parse():
     p.add_argument("--gemv-iters", type=int, default=50)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip configs 1, 3, 4 and 5")
-    p.add_argument("--profile", choices=["gemv", "prefill", "midrows"], default=None)
+    p.add_argument("--profile", choices=["gemv", "prefill", "midrows", "floor"], default=None)
     return p.parse_args()
 
 
@@ -165,6 +165,11 @@ def gemv_roofline(iters):
     tot_bytes = sum(v["bytes"] for v in per.values())
     tot_us = sum(v["avg_us"] for v in per.values())
     achieved = tot_bytes / (tot_us * 1e3)
+    # what a plain streaming read of the same three sizes takes, same timing
+    fl = read_floor_fixed()
+    floor = {"us_per_set": round(sum(fl.values()), 2), "launches_us": fl,
+             "frac": round(tot_bytes / (sum(fl.values()) * 1e3) / HBM_PEAK_GBS, 4),
+             "set_vs_floor": round(sum(fl.values()) / tot_us, 4)}
     # the PMC traffic figure counts only when it was measured on this build's
     # kernel sources (profiles/q4_gemv_traffic.json records their hash)
     traffic = None
@@ -176,7 +181,8 @@ def gemv_roofline(iters):
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "kernel": "q4_gemv_mfma_kernel (six-linear set, 3 launches, GEMV layout)",
-            "bytes_per_set": tot_bytes, "us_per_set": round(tot_us, 2), "launches": per}
+            "bytes_per_set": tot_bytes, "us_per_set": round(tot_us, 2), "launches": per,
+            "read_floor": floor}
 
 
 def profile_gemv(iters):
@@ -192,6 +198,62 @@ def profile_gemv(iters):
         b.copy_(a)
     torch.cuda.synchronize()
     print(json.dumps({"profile": "gemv", "iters": iters, "copy_bytes_read": a.numel() * 4}))
+
+
+FLOOR_GEOMETRY = {"qkv": (14176256, 2, 8), "gate_up": (66125824, 8, 8), "down": (33067008, 8, 8)}
+
+
+def read_floor_fixed():
+    """The plain-read floor at the best geometry ``read_floor`` found per
+    launch (MI355X): bytes, workgroups per CU, loads in flight."""
+    import torch
+    from lokahi_amd import _abi
+    from lokahi_amd.ops import _ctx, _stream
+    lib = _abi.load()
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    res = {}
+    for name, (nbytes, wpc, u) in FLOOR_GEOMETRY.items():
+        bufs = [torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(i + 1)
+                for i in range(6)]
+
+        def fn(i):
+            _abi.check(lib.strata_bench_read(_ctx(0), bufs[i % 6].data_ptr(), nbytes, wpc, u,
+                                             sink.data_ptr(), _stream(0)))
+        res[name] = round(graph_time_us(fn, 48), 3)
+        del bufs
+    return res
+
+
+def read_floor():
+    """Plain-read floor of the six-linear set's three launches: the library's
+    streaming-read helper (``strata_bench_read``) over buffers of the
+    launches' sizes, 6 copies cycled (past the last-level cache), graph-timed
+    like the roofline leg, best over 2-8 workgroups per CU and 4-16 loads in
+    flight per lane."""
+    import torch
+    from lokahi_amd import _abi
+    from lokahi_amd.ops import _ctx, _stream
+    lib = _abi.load()
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    res = {}
+    for name, nbytes in (("qkv", 14176256), ("gate_up", 66125824), ("down", 33067008)):
+        bufs = [torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(i + 1)
+                for i in range(6)]
+        best = None
+        for wpc in (2, 4, 8):
+            for u in (4, 8, 16):
+                def fn(i, wpc=wpc, u=u):
+                    _abi.check(lib.strata_bench_read(_ctx(0), bufs[i % 6].data_ptr(), nbytes, wpc,
+                                                     u, sink.data_ptr(), _stream(0)))
+                us = graph_time_us(fn, 48)
+                if best is None or us < best[0]:
+                    best = (us, wpc, u)
+        res[name] = {"bytes": nbytes, "us": round(best[0], 2), "wg_per_cu": best[1],
+                     "loads_in_flight": best[2], "GBps": round(nbytes / best[0] / 1e3, 1)}
+        del bufs
+    res["set_us"] = round(sum(v["us"] for v in res.values() if isinstance(v, dict)), 2)
+    res["set_frac_hbm"] = round(113369088 / res["set_us"] / 1e3 / HBM_PEAK_GBS, 4)
+    return res
 
 
 def profile_prefill(iters=3):
@@ -520,6 +582,9 @@ def main():
                                    "run with --gpus 1"}))
         sys.exit(2)
     import torch
+    if args.profile == "floor":
+        print(json.dumps({"profile": "floor", "read_floor": read_floor()}))
+        return
     if args.profile == "gemv":
         profile_gemv(args.gemv_iters)
         return

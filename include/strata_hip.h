@@ -297,6 +297,17 @@ int strata_decoder_forward(strata_decoder* dec, const int32_t* ids, int B, int L
 int strata_decoder_generate(strata_decoder* dec, const int32_t* prompt, int B, int L, int max_new,
                             float temperature, int use_graph, int32_t* out_tokens, void* stream);
 
+/* ------------------------------------------------------ measurement helper
+ * No counterpart in the reference: the plain-read floor the decode GEMV is
+ * measured against.  Streams `bytes` (a multiple of 16) from the device
+ * buffer p with 16-byte loads, `unroll` (4, 8 or 16) loads in flight per
+ * lane, num_cus * wg_per_cu (1..16) workgroups of 256 threads striding over
+ * the buffer; the loaded words are folded and written to sink (16 bytes,
+ * device) only if they fold to a constant, so in practice nothing is
+ * written.  No other work: its duration is what reading the bytes costs. */
+int strata_bench_read(strata_ctx* ctx, const void* p, int64_t bytes, int wg_per_cu, int unroll,
+                      void* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,8 @@ _SIGS = {
     "strata_q4_layout_create": ([C.c_void_p, C.POINTER(Q4Weight), C.c_int, C.c_int64, c_void_pp],
                                 C.c_int),
     "strata_q4_layout_destroy": ([C.c_void_p], C.c_int),
+    "strata_bench_read": ([C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p,
+                           C.c_void_p], C.c_int),
     "strata_linear_q4_layout": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int64, C.c_void_p,
                                  C.POINTER(C.c_void_p), C.c_int, C.c_void_p], C.c_int),
     "strata_linear_bf16": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_void_p,

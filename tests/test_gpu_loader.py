@@ -45,3 +45,25 @@ def test_loaded_checkpoint_generates_oracle_tokens(dev, tmp_path, embed, head, s
     got = model.generate(torch.from_numpy(prompt), max_new_tokens=12).cpu().numpy()
     exp = oll.greedy_generate(ref, prompt, max_new_tokens=12, cache=OracleKVCache(3))
     assert np.array_equal(got, exp), f"\n{got}\n{exp}"
+
+
+MID = oll.Config(vocab_size=1024, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                 num_attention_heads=4, num_key_value_heads=2, rms_norm_eps=1e-5,
+                 rope_theta=500000.0)
+
+
+def test_q4_head_with_prefill_pack_generates_oracle_tokens(dev, tmp_path):
+    """A q4 lm_head set after the engine re-laid its prefill linears (every
+    linear's N a multiple of 256, a 48-token prompt: the prefill runs the
+    MFMA GEMM on the load-time layout), then greedy decode on the q4 head's
+    GEMV layout; the oracle's smallest top-2 gap over the 8 tokens is 0.148
+    at seed 60."""
+    from lokahi_amd.loader import load_mlx_llama
+    hw = oll.random_weights(MID, seed=60, std=0.05)
+    ow = mlx_checkpoint.export(tmp_path, MID, hw, embed="bf16", head="q4")
+    model = load_mlx_llama(tmp_path, device=0)
+    ref = oll.OracleLlama(MID, ow)
+    prompt = np.random.default_rng(60).integers(0, MID.vocab_size, (1, 48))
+    got = model.generate(torch.from_numpy(prompt), max_new_tokens=8).cpu().numpy()
+    exp = oll.greedy_generate(ref, prompt, max_new_tokens=8, cache=OracleKVCache(2))
+    assert np.array_equal(got, exp), f"\n{got}\n{exp}"
