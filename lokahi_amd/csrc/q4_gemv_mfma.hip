@@ -632,6 +632,8 @@ int strata_gemv_layout_run(const GemvLayout& L, const void* x, int M, void* cons
     a.norm_w = e->norm_w;
     a.eps = e->eps;
   }
+  STRATA_REQUIRE(mode == 0 || y_dtype == STRATA_BF16,
+                 "GEMV layout: the fused epilogues write bf16 (y_dtype %d)", y_dtype);
   STRATA_REQUIRE((mode == 1) == (L.perm == 1) && (mode == 2) == (L.perm == 2),
                  "GEMV layout: epilogue %d does not match the layout's row order %d", mode, L.perm);
   if (mode == 2)
