@@ -114,6 +114,12 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   constexpr int MM = MP == 0 ? 1 : 4;  // staged batch rows
   extern __shared__ uint4 smem[];
   const int nt = NTC ? NTC : a.nt, M = a.M, K = a.K;
+  // Every kernel argument the load issue below needs, in SGPRs at once: one
+  // wait for the argument loads instead of one per field between the loads.
+  const uint4* const codes = a.codes;
+  const uint4* const sbp = a.sb;
+  const uint16_t* const nw = NORM ? a.norm_w : nullptr;
+  asm volatile("" ::"s"(codes), "s"(sbp), "s"(nw), "s"(M), "s"(K), "s"(nt));
   const int lane = threadIdx.x & 63, j = lane >> 4, n = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rb = blockIdx.x;
@@ -140,7 +146,7 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int k = 1024 * t + 8 * (lane + 64 * e);
-      wn[e] = k < K ? *reinterpret_cast<const uint4*>(a.norm_w + k) : make_uint4(0, 0, 0, 0);
+      wn[e] = k < K ? *reinterpret_cast<const uint4*>(nw + k) : make_uint4(0, 0, 0, 0);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -150,13 +156,13 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   {
     const int64_t tb = (int64_t)rb * nt + t;
     if constexpr (MP == 0) {
-      sbv[0] = load_nt(a.sb + tb * 64 + lane);
+      sbv[0] = load_nt(sbp + tb * 64 + lane);
     } else {
 #pragma unroll
-      for (int ph = 0; ph < 4; ++ph) sbv[ph] = load_nt(a.sb + tb * 64 + 16 * j + 4 * ph + (lane & 3));
+      for (int ph = 0; ph < 4; ++ph) sbv[ph] = load_nt(sbp + tb * 64 + 16 * j + 4 * ph + (lane & 3));
     }
 #pragma unroll
-    for (int w = 0; w < 8; ++w) wb[w] = load_nt(a.codes + (tb * 8 + w) * 64 + lane);
+    for (int w = 0; w < 8; ++w) wb[w] = load_nt(codes + (tb * 8 + w) * 64 + lane);
   }
   __builtin_amdgcn_sched_barrier(0);
 
