@@ -105,13 +105,18 @@ constexpr int kWaveLds = MM * 2048 + 256 + MM * 64;
 template <int MP, int EPI>
 constexpr int kGvWavesPerEu = MP != 0 ? 2 : (EPI == 2 ? 4 : 7);
 
-// NTC: the K task count (waves per workgroup) when known at compile time
-// (4: the 8B hidden width, 14: the 8B FFN width, 3 and 8: the 3B widths),
-// 0 for any (up to 16).
-template <int MP, int EPI, bool NORM, typename YT, int NTC>
-__global__ __launch_bounds__(NTC ? 64 * NTC : 1024) __attribute__((amdgpu_waves_per_eu(kGvWavesPerEu<MP, EPI>)))
+// NTC: the K task count when known at compile time (4: the 8B hidden width,
+// 14: the 8B FFN width, 3 and 8: the 3B widths), 0 for any (up to 16).
+// HT: waves per K task.  With HT = 2 (batch 1, launches too small to fill
+// the GPU) each wave takes half a task, 4 of its 8 weight loads and 2 of its
+// 4 phases, so the block has twice the waves, each with half the chain.
+template <int MP, int EPI, bool NORM, typename YT, int NTC, int HT = 1>
+__global__ __launch_bounds__(NTC ? 64 * NTC * HT : 1024) __attribute__((amdgpu_waves_per_eu(kGvWavesPerEu<MP, EPI>)))
 void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
+  static_assert(HT == 1 || (HT == 2 && MP == 0), "half tasks are batch-1 only");
   constexpr int MM = MP == 0 ? 1 : 4;  // staged batch rows
+  constexpr int NE = 2 / HT;           // x uint4 per lane of the wave's (half) task
+  constexpr int NWL = 8 / HT;          // weight loads per lane
   extern __shared__ uint4 smem[];
   const int nt = NTC ? NTC : a.nt, M = a.M, K = a.K;
   // Every kernel argument the load issue below needs, in SGPRs at once: one
@@ -123,35 +128,40 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   const int lane = threadIdx.x & 63, j = lane >> 4, n = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rb = blockIdx.x;
-  const int t = wave;  // this wave's K task
+  const int t = HT == 2 ? wave >> 1 : wave;  // this wave's K task
+  const int hh = HT == 2 ? wave & 1 : 0;     // and its half (HT = 2)
+  const int nw_ = nt * HT;                   // waves of the block
   char* base = reinterpret_cast<char*>(smem);
   uint4* xw = reinterpret_cast<uint4*>(base + wave * kWaveLds<MM>);
   uint4* zero = xw + MM * 128;
   float* xs = reinterpret_cast<float*>(zero + 16);
-  float* red = reinterpret_cast<float*>(base + nt * kWaveLds<MM>);  // [nt][MM][16]
-  float* nred = red + nt * MM * 16;                                 // [nt][MM]
+  float* red = reinterpret_cast<float*>(base + nw_ * kWaveLds<MM>);  // [waves][MM][16]
+  float* nred = red + nw_ * MM * 16;                                  // [waves][MM]
 
   // x of the task: uint4 u (0..127) = x[8u .. 8u+7] of the task, group u / 8.
-  uint4 xv[MM][2], wn[2];
+  // (HT = 2: the wave's half hh holds u = 64 hh + lane, one per lane)
+  uint4 xv[MM][NE], wn[NE];
 #pragma unroll
   for (int m = 0; m < MM; ++m)
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int ee = 0; ee < NE; ++ee) {
+      const int e = HT == 2 ? hh : ee;
       const int k = 1024 * t + 8 * (lane + 64 * e);
       const int mc = min(m, M - 1);
-      xv[m][e] = k < K ? *reinterpret_cast<const uint4*>(x + (int64_t)mc * K + k)
-                       : make_uint4(0, 0, 0, 0);
+      xv[m][ee] = k < K ? *reinterpret_cast<const uint4*>(x + (int64_t)mc * K + k)
+                        : make_uint4(0, 0, 0, 0);
     }
   if constexpr (NORM) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int ee = 0; ee < NE; ++ee) {
+      const int e = HT == 2 ? hh : ee;
       const int k = 1024 * t + 8 * (lane + 64 * e);
-      wn[e] = k < K ? *reinterpret_cast<const uint4*>(nw + k) : make_uint4(0, 0, 0, 0);
+      wn[ee] = k < K ? *reinterpret_cast<const uint4*>(nw + k) : make_uint4(0, 0, 0, 0);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
   // weights and affine terms of the task, all issued before any math
-  uint4 wb[8];
+  uint4 wb[NWL];
   uint4 sbv[MP == 0 ? 1 : 4];
   {
     const int64_t tb = (int64_t)rb * nt + t;
@@ -162,7 +172,7 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
       for (int ph = 0; ph < 4; ++ph) sbv[ph] = load_nt(sbp + tb * 64 + 16 * j + 4 * ph + (lane & 3));
     }
 #pragma unroll
-    for (int w = 0; w < 8; ++w) wb[w] = load_nt(codes + (tb * 8 + w) * 64 + lane);
+    for (int w = 0; w < NWL; ++w) wb[w] = load_nt(codes + (tb * 8 + 4 * hh + w) * 64 + lane);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -203,7 +213,8 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
 #pragma unroll
   for (int m = 0; m < MM; ++m)
 #pragma unroll
-    for (int e = 0; e < 2; ++e) xw[m * 128 + lane + 64 * e] = m < M ? xv[m][e] : make_uint4(0, 0, 0, 0);
+    for (int ee = 0; ee < NE; ++ee)
+      xw[m * 128 + lane + 64 * (HT == 2 ? hh : ee)] = m < M ? xv[m][ee] : make_uint4(0, 0, 0, 0);
   // RMSNorm prologue (llama_mlx.py:77-92): r = 1/sqrt(mean(x^2) + eps) over
   // the whole row (the block's waves together hold it), then
   // x <- bf16(w * (x * r)) with each product rounded.
@@ -212,8 +223,8 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
     for (int m = 0; m < MM; ++m) {
       float sq = 0.f;
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const uint32_t u[4] = {xv[m][e].x, xv[m][e].y, xv[m][e].z, xv[m][e].w};
+      for (int ee = 0; ee < NE; ++ee) {
+        const uint32_t u[4] = {xv[m][ee].x, xv[m][ee].y, xv[m][ee].z, xv[m][ee].w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const float lo = __uint_as_float(u[c] << 16), hi = __uint_as_float(u[c] & 0xffff0000u);
@@ -228,13 +239,14 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
       float tot = 0.f;
-      for (int w = 0; w < nt; ++w) tot += nred[w * MM + m];
+      for (int w = 0; w < nw_; ++w) tot += nred[w * MM + m];
       const float r = 1.0f / sqrtf(tot / static_cast<float>(K) + a.eps);
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
+      for (int ee = 0; ee < NE; ++ee) {
+        const int e = HT == 2 ? hh : ee;
         uint4 v = xw[m * 128 + lane + 64 * e];
         uint32_t* u = reinterpret_cast<uint32_t*>(&v);
-        const uint32_t wu[4] = {wn[e].x, wn[e].y, wn[e].z, wn[e].w};
+        const uint32_t wu[4] = {wn[ee].x, wn[ee].y, wn[ee].z, wn[ee].w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const float lo = mul_rn(mul_rn(__uint_as_float(u[c] << 16), r), __uint_as_float(wu[c] << 16));
@@ -250,7 +262,8 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
 #pragma unroll
   for (int m = 0; m < MM; ++m)
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int ee = 0; ee < NE; ++ee) {
+      const int e = HT == 2 ? hh : ee;
       const uint4 v = xw[m * 128 + lane + 64 * e];
       const uint32_t u[4] = {v.x, v.y, v.z, v.w};
       float s = 0.f;
@@ -280,19 +293,26 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   };
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   if constexpr (MP == 0) {
-    const uint4* bb[4];
+    // the wave's phases: 4 (HT = 1), or 2 hh .. 2 hh + 1 (HT = 2)
+    constexpr int NPH = 4 / HT;
+    const uint4* bb[NPH];
 #pragma unroll
-    for (int ph = 0; ph < 4; ++ph) bb[ph] = (n == 4 * ph + j) ? xw + (4 * ph + j) * 8 : zero;
+    for (int q = 0; q < NPH; ++q) {
+      const int ph = NPH * hh + q;
+      bb[q] = (n == 4 * ph + j) ? xw + (4 * ph + j) * 8 : zero;
+    }
     f32x4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int p = 0; p < 32; ++p) {
+    for (int p = 0; p < 8 * NPH; ++p) {
       const u32x4_t av = a_op(p);
       const uint4 bv = bb[p >> 3][p & 7];
       const u32x4_t bq = {bv.x, bv.y, bv.z, bv.w};
       if (p & 1) c1 = mfma16(av, bq, c1);
       else c0 = mfma16(av, bq, c0);
     }
-    const float X = xs[n];
+    // group column n belongs to phase n / 4: columns of the other half's
+    // phases hold no product and get no affine term
+    const float X = (HT == 1 || (n >> 3) == hh) ? xs[n] : 0.f;
     const uint32_t sw[4] = {sbv[0].x, sbv[0].y, sbv[0].z, sbv[0].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -355,7 +375,7 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   // the K tasks of the block summed in task order (deterministic)
   auto total = [&](int row) {
     float s = 0.f;
-    for (int w = 0; w < nt; ++w) s += red[(w * MM + (MP == 0 ? 0 : em)) * 16 + row];
+    for (int w = 0; w < nw_; ++w) s += red[(w * MM + (MP == 0 ? 0 : em)) * 16 + row];
     return s;
   };
   const GvProblem& P = a.p[pi];
@@ -496,30 +516,44 @@ __global__ void q4_gemv_pack_sb(GvPackArgs a, uint32_t* __restrict__ sb) {
   }
 }
 
+// Batch-1 launches with fewer than kGvHalfTaskWaves task waves run half
+// tasks (HT = 2): twice the waves, each with half the load-to-store chain.
+constexpr int64_t kGvHalfTaskWaves = 4096;
+
+template <int MP, int EPI, bool NORM, typename YT, int NTC, int HT>
+void launch_one(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
+  constexpr int MM = MP == 0 ? 1 : 4;
+  const int waves = a.nt * HT;
+  const size_t lds = (size_t)waves * (kWaveLds<MM> + MM * 64 + MM * 4);
+  hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, NTC, HT>), dim3(nrb), dim3(64 * waves),
+                     lds, st, x, a);
+}
+
 template <int MP, int EPI, bool NORM, typename YT>
 void launch_gv(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
-  constexpr int MM = MP == 0 ? 1 : 4;
-  const size_t lds = (size_t)a.nt * (kWaveLds<MM> + MM * 64 + MM * 4);
+  const bool half = MP == 0 && (int64_t)nrb * a.nt < kGvHalfTaskWaves;
   if (a.nt == 4) {
-    hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 4>), dim3(nrb), dim3(256), lds, st, x, a);
+    if (half) launch_one<MP, EPI, NORM, YT, 4, MP == 0 ? 2 : 1>(x, a, nrb, st);
+    else launch_one<MP, EPI, NORM, YT, 4, 1>(x, a, nrb, st);
     return;
   }
   if (a.nt == 14 && !NORM) {
-    hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 14>), dim3(nrb), dim3(896), lds, st, x, a);
+    launch_one<MP, EPI, NORM, YT, 14, 1>(x, a, nrb, st);
     return;
   }
   if constexpr (MP == 0) {  // batch 1 at the 3B widths (3072, and 8192 for down)
     if (a.nt == 3) {
-      hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 3>), dim3(nrb), dim3(192), lds, st, x, a);
+      if (half) launch_one<MP, EPI, NORM, YT, 3, 2>(x, a, nrb, st);
+      else launch_one<MP, EPI, NORM, YT, 3, 1>(x, a, nrb, st);
       return;
     }
     if (a.nt == 8 && !NORM) {
-      hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 8>), dim3(nrb), dim3(512), lds, st, x, a);
+      if (half) launch_one<MP, EPI, NORM, YT, 8, 2>(x, a, nrb, st);
+      else launch_one<MP, EPI, NORM, YT, 8, 1>(x, a, nrb, st);
       return;
     }
   }
-  hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, 0>), dim3(nrb), dim3(64 * a.nt), lds, st,
-                     x, a);
+  launch_one<MP, EPI, NORM, YT, 0, 1>(x, a, nrb, st);
 }
 
 template <int EPI, bool NORM, typename YT>
