@@ -30,6 +30,21 @@ int strata_bf16_gemv(strata_ctx* ctx, const void* x, int M, int K, const uint16_
   hipStream_t s = as_stream(stream);
   const uint16_t* xx = reinterpret_cast<const uint16_t*>(x);
   const uint4* ww = reinterpret_cast<const uint4*>(w);
+  if (MT == 1 && K >= 4096) {
+    // batch 1, K >= 4096: 16 waves per workgroup, x staged after the first
+    // weight loads (8B lm_head, 1.05 GB: 159 -> 152-153 us against 8 waves
+    // with x first; the 3B head, K = 3072, stays on 8 waves: 112 against 114 us)
+    constexpr int NW1 = 16;
+    const dim3 g1((N + NW1 - 1) / NW1);
+    if (y_dtype == STRATA_F32)
+      hipLaunchKernelGGL((bf16_gemv_kernel<NW1, 1, U, 1, float, 0>), g1, dim3(NW1 * 64), lds, s, xx,
+                         M, K, ww, N, reinterpret_cast<float*>(y));
+    else
+      hipLaunchKernelGGL((bf16_gemv_kernel<NW1, 1, U, 1, bf16_t, 0>), g1, dim3(NW1 * 64), lds, s, xx,
+                         M, K, ww, N, reinterpret_cast<bf16_t*>(y));
+    STRATA_HIP_CHECK(hipGetLastError());
+    return STRATA_OK;
+  }
   // x ahead of the weights when each batch row is one uint4 per thread
   // (K = 4096: the lm_head of the Llama-3-8B shape)
   const int xi = K / 8 == NW * 64 ? MT : 0;
