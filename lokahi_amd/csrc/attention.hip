@@ -1181,14 +1181,18 @@ __global__ __launch_bounds__(64) void attn_generic(
 // At batch 1 the kernel is bound by each wave's dependent chain, so short
 // splits (more waves) win up to ~2.3k keys (2k: 7.6 us against 8.2 us); from
 // 4k keys two sweeps per split halve the merge's work (4k: 10.1 us against
-// 11.4 us; 8k: 15.5 us against 17.4 us) (STRATA_ATTN_MIN_CHUNK overrides the
-// minimum).
+// 11.4 us; 8k: 15.5 us against 17.4 us).
 constexpr int kLongSplitKeys = 3072;    // 128-key minimum split from here
 constexpr int kLongContextKeys = 6144;  // few heads: 2 splits per CU from here
 constexpr int kBatchedShortKeys = 2048; // batched heads: 2 per CU up to here
 constexpr int kBatchedLongKeys = 16384; // batched heads: 6 per CU from here
-void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out) {
-  int min_chunk = Lcap >= kLongSplitKeys ? 128 : 64;
+void decode_split_geometry(int num_cus, int B, int Hkv, int Lcap, int* nsplit_out, int* chunk_out,
+                           bool whole_group = false) {
+  // A query group that cannot be halved over workgroups (odd G > 1, e.g.
+  // Llama-3.2-3B's G = 3) also takes 128-key splits at short contexts
+  // (3B decode at ~2k keys: 963 -> 971 tok/s; G = 4 keeps 64: 8B 649
+  // against 629 tok/s with 128).
+  int min_chunk = (Lcap >= kLongSplitKeys || whole_group) ? 128 : 64;
   // Batched heads (B*Hkv >= 64, e.g. 16 x 8): short contexts prefer longer
   // splits (1k keys: 21.6 us at 2 per CU against 24.0 at 4), very long ones
   // more of them (32k keys: 371 us at 6 against 378 at 4).  Few heads (batch
@@ -1281,7 +1285,7 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
     }
   }
   int nsplit, chunk;
-  decode_split_geometry(ctx->num_cus, B, Hkv, Lk, &nsplit, &chunk);
+  decode_split_geometry(ctx->num_cus, B, Hkv, Lk, &nsplit, &chunk, G > 1 && G % 2 != 0);
   float* part = nullptr;
   if (nsplit > 1) {
     if (ex.part) {  // decoder-owned partials (graph-safe: no allocation)
