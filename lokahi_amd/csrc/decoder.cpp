@@ -184,7 +184,7 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
     RC(strata_q4_gemm_multi(d->ctx, d->xn, T, H, qkv, 3, STRATA_BF16, stream, pk ? &pk[0] : nullptr));
     RC(strata_rope_kv_fused_launch(d->q, d->k, d->v, STRATA_BF16, B, Hq, Hkv, L, D, kv->Lmax,
                                    pos0, nullptr, c.rope_theta, d->qr, kc, vc, STRATA_BF16,
-                                   stream));
+                                   stream, d->rope_table));
     AttnExtra ex;
     ex.out_tm = 1;  // prefill writes [B, L, Hq, D], the o_proj input layout
     RC(strata_attention_dispatch(d->ctx, d->qr, STRATA_BF16, kc, STRATA_BF16, vc, STRATA_BF16,

@@ -14,7 +14,7 @@
 // preallocated [B, Hkv, Lmax, D] buffer per layer.
 #include <algorithm>
 
-#include "strata_common.h"
+#include "strata_internal.h"
 
 namespace {
 
@@ -64,7 +64,8 @@ template <typename TS, typename TC>
 __global__ void rope_kv_fused(const TS* __restrict__ qs, const TS* __restrict__ ks,
                               const TS* __restrict__ vs, int B, int Hq, int Hkv, int L, int D,
                               int Lmax, int pos0, const int* __restrict__ dpos, float theta,
-                              TS* __restrict__ q_out, TC* __restrict__ kc, TC* __restrict__ vc) {
+                              TS* __restrict__ q_out, TC* __restrict__ kc, TC* __restrict__ vc,
+                              const float2* __restrict__ table) {
   // dpos (device) overrides pos0: the decode step replayed from a HIP graph
   // reads its position from memory the previous step advanced.
   if (dpos) pos0 = *dpos;
@@ -79,7 +80,15 @@ __global__ void rope_kv_fused(const TS* __restrict__ qs, const TS* __restrict__ 
     const int b = r / L;
     const int pos = pos0 + l;
     float c = 0.f, s = 0.f;
-    if ((int)blockIdx.y < Hq + Hkv) rope_cs(pos, i, D, theta, &c, &s);
+    if ((int)blockIdx.y < Hq + Hkv) {
+      if (table) {  // the same values, built once by rope_cs
+        const float2 cs = table[(int64_t)pos * half + i];
+        c = cs.x;
+        s = cs.y;
+      } else {
+        rope_cs(pos, i, D, theta, &c, &s);
+      }
+    }
     for (int h = blockIdx.y; h < NH; h += gridDim.y) {
       if (h < Hq) {
         const int64_t so = ((int64_t)b * L + l) * Hq * D + (int64_t)h * D;
@@ -109,6 +118,78 @@ __global__ void rope_kv_fused(const TS* __restrict__ qs, const TS* __restrict__ 
         Elem<TC>::store(vc, co + i, Elem<TS>::load(vs, so + i));
         Elem<TC>::store(vc, co + i + half, Elem<TS>::load(vs, so + i + half));
       }
+    }
+  }
+}
+
+// The bf16 fused kernel with a (cos, sin) table, 8 pairs per thread: a
+// thread owns (b, l, 8-pair chunk) and moves 16 bytes per load and store;
+// the same arithmetic per pair as rope_kv_fused.  D % 16 == 0, 16-byte
+// aligned operands.
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__global__ void rope_kv_fused_v8(const uint16_t* __restrict__ qs, const uint16_t* __restrict__ ks,
+                                 const uint16_t* __restrict__ vs, int B, int Hq, int Hkv, int L,
+                                 int D, int Lmax, int pos0, const int* __restrict__ dpos,
+                                 uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
+                                 uint16_t* __restrict__ vc, const float2* __restrict__ table) {
+  if (dpos) pos0 = *dpos;
+  const int half = D / 2, nc = half / 8;
+  const int NH = Hq + 2 * Hkv;
+  const int64_t total = (int64_t)B * L * nc;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int i0 = 8 * (int)(idx % nc);
+    const int64_t r = idx / nc;
+    const int l = r % L;
+    const int b = r / L;
+    const int pos = pos0 + l;
+    float c[8], sn[8];
+    if ((int)blockIdx.y < Hq + Hkv) {
+      const float4* tp = reinterpret_cast<const float4*>(table + (int64_t)pos * half + i0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 t = tp[q];
+        c[2 * q] = t.x;
+        sn[2 * q] = t.y;
+        c[2 * q + 1] = t.z;
+        sn[2 * q + 1] = t.w;
+      }
+    }
+    for (int h = blockIdx.y; h < NH; h += gridDim.y) {
+      const uint16_t* src;
+      uint16_t* dst;
+      int64_t so;
+      if (h < Hq) {
+        so = ((int64_t)b * L + l) * Hq * D + (int64_t)h * D;
+        src = qs;
+        dst = q_out + (((int64_t)b * Hq + h) * L + l) * D;
+      } else {
+        const int hk = h < Hq + Hkv ? h - Hq : h - Hq - Hkv;
+        so = ((int64_t)b * L + l) * Hkv * D + (int64_t)hk * D;
+        src = h < Hq + Hkv ? ks : vs;
+        dst = (h < Hq + Hkv ? kc : vc) + (((int64_t)b * Hkv + hk) * Lmax + pos) * D;
+      }
+      const uint4 a = *reinterpret_cast<const uint4*>(src + so + i0);
+      const uint4 e = *reinterpret_cast<const uint4*>(src + so + i0 + half);
+      if (h >= Hq + Hkv) {  // V: copied
+        *reinterpret_cast<uint4*>(dst + i0) = a;
+        *reinterpret_cast<uint4*>(dst + i0 + half) = e;
+        continue;
+      }
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, ew[4] = {e.x, e.y, e.z, e.w};
+      uint32_t o1w[4], o2w[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float p1, p2, r1, r2;
+        rotate_pair(bf_lo(aw[q]), bf_lo(ew[q]), c[2 * q], sn[2 * q], &p1, &p2);
+        rotate_pair(bf_hi(aw[q]), bf_hi(ew[q]), c[2 * q + 1], sn[2 * q + 1], &r1, &r2);
+        o1w[q] = (uint32_t)f32_to_bf16(p1) | ((uint32_t)f32_to_bf16(r1) << 16);
+        o2w[q] = (uint32_t)f32_to_bf16(p2) | ((uint32_t)f32_to_bf16(r2) << 16);
+      }
+      *reinterpret_cast<uint4*>(dst + i0) = make_uint4(o1w[0], o1w[1], o1w[2], o1w[3]);
+      *reinterpret_cast<uint4*>(dst + i0 + half) = make_uint4(o2w[0], o2w[1], o2w[2], o2w[3]);
     }
   }
 }
@@ -164,7 +245,7 @@ int strata_kv_copy_launch(const void* src, int src_dtype, void* dst, int dst_dty
 int strata_rope_kv_fused_launch(const void* qs, const void* ks, const void* vs, int src_dtype,
                                 int B, int Hq, int Hkv, int L, int D, int Lmax, int pos0,
                                 const int* dpos, float theta, void* q_out, void* kc, void* vc,
-                                int cache_dtype, void* stream) {
+                                int cache_dtype, void* stream, const void* rope_table) {
   hipStream_t s = as_stream(stream);
   // Heads are dealt over grid.y: all of them for short inputs (as many
   // threads as elements), slices of 6 from 256 rows, so (cos, sin) is
@@ -173,14 +254,21 @@ int strata_rope_kv_fused_launch(const void* qs, const void* ks, const void* vs, 
   const int64_t rows = (int64_t)B * L;
   const int hy = rows >= 256 ? std::max(1, (NH + 5) / 6) : NH;
   const dim3 g(grid_for(rows * (D / 2)), hy), blk(256);
-  if (src_dtype == STRATA_BF16 && cache_dtype == STRATA_BF16)
+  const bool v8 = rope_table && D % 16 == 0 && aligned16(qs) && aligned16(ks) && aligned16(vs) &&
+                  aligned16(q_out) && aligned16(kc) && aligned16(vc);
+  if (src_dtype == STRATA_BF16 && cache_dtype == STRATA_BF16 && v8) {
+    const dim3 g8(grid_for(rows * (D / 16)), hy);
+    hipLaunchKernelGGL(rope_kv_fused_v8, g8, blk, 0, s, (const uint16_t*)qs, (const uint16_t*)ks,
+                       (const uint16_t*)vs, B, Hq, Hkv, L, D, Lmax, pos0, dpos, (uint16_t*)q_out,
+                       (uint16_t*)kc, (uint16_t*)vc, (const float2*)rope_table);
+  } else if (src_dtype == STRATA_BF16 && cache_dtype == STRATA_BF16)
     hipLaunchKernelGGL((rope_kv_fused<bf16_t, bf16_t>), g, blk, 0, s, (const bf16_t*)qs,
                        (const bf16_t*)ks, (const bf16_t*)vs, B, Hq, Hkv, L, D, Lmax, pos0, dpos, theta,
-                       (bf16_t*)q_out, (bf16_t*)kc, (bf16_t*)vc);
+                       (bf16_t*)q_out, (bf16_t*)kc, (bf16_t*)vc, (const float2*)rope_table);
   else if (src_dtype == STRATA_F32 && cache_dtype == STRATA_F32)
     hipLaunchKernelGGL((rope_kv_fused<float, float>), g, blk, 0, s, (const float*)qs,
                        (const float*)ks, (const float*)vs, B, Hq, Hkv, L, D, Lmax, pos0, dpos, theta,
-                       (float*)q_out, (float*)kc, (float*)vc);
+                       (float*)q_out, (float*)kc, (float*)vc, (const float2*)rope_table);
   else
     return strata_set_error(STRATA_ENOTSUP,
                             "rope_kv_append: source and cache dtypes must match");

@@ -127,7 +127,7 @@ int strata_kv_copy_launch(const void* src, int src_dtype, void* dst, int dst_dty
 int strata_rope_kv_fused_launch(const void* qs, const void* ks, const void* vs, int src_dtype,
                                 int B, int Hq, int Hkv, int L, int D, int Lmax, int pos0,
                                 const int* dpos, float theta, void* q_out, void* kc, void* vc,
-                                int cache_dtype, void* stream);
+                                int cache_dtype, void* stream, const void* rope_table = nullptr);
 int strata_rmsnorm_launch(void* x, const void* res, const uint16_t* w, int64_t rows, int64_t H,
                           float eps, void* y, void* stream);
 int strata_silu_mul_launch(const void* g, const void* u, int64_t n, void* a, void* stream);

@@ -59,3 +59,18 @@ def test_argmax_ties_pick_lowest_index(dev):
     assert out.tolist() == [int(np.argmax(lg[0])), 7, 0]
     small = np.array([[0.0, 2.0, 2.0, -1.0]], np.float32)
     assert ops.argmax(torch.from_numpy(small).to(dev)).cpu().numpy().tolist() == [1]
+
+
+def test_silu_mul_vector_and_scalar_paths_agree_bit_for_bit(dev):
+    """16-byte path (aligned, n % 8 == 0) and per-element path (an odd length
+    at an odd offset) run the same arithmetic per value."""
+    from lokahi_amd import ops
+    rng = np.random.default_rng(3)
+    g = round_bf16(rng.normal(0, 4, 40008).astype(np.float32))
+    u = round_bf16(rng.normal(size=40008).astype(np.float32))
+    tg, tu = bf16_dev(g, dev), bf16_dev(u, dev)
+    vec = bits(ops.silu_mul(tg, tu))
+    sca = bits(ops.silu_mul(tg[1:40002], tu[1:40002]))
+    assert np.array_equal(vec[1:40002], sca)
+    ref = oll.silu_mul(g, u)
+    assert np.mean(vec == f32_to_bf16_bits(ref)) > 0.995

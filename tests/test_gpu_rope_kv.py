@@ -153,3 +153,27 @@ def test_fused_rope_kv_append_long_rows_matches_oracle(dev):
         assert np.array_equal(bits(V), f32_to_bf16_bits(rv))
         pos0 += L
     assert cache.get_seq_length(0) == 301
+
+
+def test_engine_prefill_rope_append_matches_op_by_op_path(dev):
+    """The engine's prefill appends RoPE'd K and V with the 16-byte kernel
+    over the (cos, sin) table; the op-by-op path uses the per-pair kernel
+    that evaluates cos/sin itself.  Layer 0 sees the same projections on
+    both paths, so its cache rows must agree bit for bit."""
+    import numpy as np
+    from lokahi_amd.llama import DecoderEngine, HipLlamaForCausalLM, LlamaConfig, weights_to_device
+    from oracle import llama as oll
+    cfg = oll.Config(vocab_size=1024, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                     num_attention_heads=4, num_key_value_heads=2)
+    lc = LlamaConfig(**{f: getattr(cfg, f) for f in cfg.__dataclass_fields__})
+    model = HipLlamaForCausalLM(lc, weights_to_device(oll.random_weights(cfg, seed=8, std=0.05)))
+    ids = torch.from_numpy(np.random.default_rng(8).integers(0, 1024, (1, 48)))
+    c1 = model.new_cache(1, 64)
+    eng = DecoderEngine(model, c1, max_batch=1, max_tokens=64)
+    eng.forward(ids)
+    c2 = model.new_cache(1, 64)
+    model(ids, past_key_values=c2, use_cache=True, logits="last")
+    k1, v1 = c1.views(0)
+    k2, v2 = c2.views(0)
+    assert torch.equal(k1[:, :, :48].cpu(), k2[:, :, :48].cpu())
+    assert torch.equal(v1[:, :, :48].cpu(), v2[:, :, :48].cpu())
