@@ -124,7 +124,7 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   const uint4* const codes = a.codes;
   const uint4* const sbp = a.sb;
   const uint16_t* const nw = NORM ? a.norm_w : nullptr;
-  asm volatile("" ::"s"(codes), "s"(sbp), "s"(nw), "s"(M), "s"(K), "s"(nt));
+  asm volatile("" ::"s"(x), "s"(codes), "s"(sbp), "s"(nw), "s"(M), "s"(K), "s"(nt));
   const int lane = threadIdx.x & 63, j = lane >> 4, n = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rb = blockIdx.x;
