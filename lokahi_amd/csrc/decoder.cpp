@@ -104,6 +104,28 @@ int alloc(void** p, size_t bytes) {
 
 constexpr int kKeyBucket = 256;
 
+// The layout GEMV over T <= 8 rows: launches of at most 4 rows (its widest
+// batch tile), each with x, the outputs and the epilogue's per-row
+// destinations advanced to its first row.
+int layout_rows(const GemvLayout& L, const void* x, int T, void* const* ys, const GemvEpilogue& e,
+                int Hq, int Hkv, int D, int lmax, void* stream) {
+  for (int r0 = 0; r0 < T; r0 += 4) {
+    const int m = std::min(4, T - r0);
+    void* y[kGvMaxProblems] = {};
+    for (int i = 0; i < L.count; ++i)
+      y[i] = ys[i] ? static_cast<uint16_t*>(ys[i]) + (int64_t)r0 * L.N[i] : nullptr;
+    GemvEpilogue er = e;
+    if (e.mode == 2 && r0 > 0) {  // q rows [B, Hq, 1, D], cache rows [B, Hkv, lmax, D]
+      er.q_out = e.q_out + (int64_t)r0 * Hq * D;
+      er.kc = e.kc + (int64_t)r0 * Hkv * lmax * D;
+      er.vc = e.vc + (int64_t)r0 * Hkv * lmax * D;
+    }
+    RC(strata_gemv_layout_run(L, static_cast<const uint16_t*>(x) + (int64_t)r0 * L.K, m, y,
+                              STRATA_BF16, &er, stream));
+  }
+  return STRATA_OK;
+}
+
 // One decoder forward over T = B*L tokens at positions pos0..pos0+L-1
 // (pos0 < 0: read from counters[1], decode graph mode, L == 1, with at most
 // `key_cap` keys per layer).
@@ -118,7 +140,7 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
   // One-token steps (T <= 8 rows) fuse RoPE/append and SiLU into GEMV epilogues.
   const bool decode = L == 1 && T <= 8;
   if (decode) {
-    const bool use_lay = !d->dlay.empty() && T <= 4;
+    const bool use_lay = !d->dlay.empty();
     // Five launches per layer; the residual stream h is updated in place by
     // the o/down epilogues, and RMSNorm runs in the q/k/v and gate/up
     // prologues:
@@ -138,7 +160,7 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
                       (uint16_t*)d->qr, (uint16_t*)kc, (uint16_t*)vc, Lw.input_norm,
                       c.rms_norm_eps, d->rope_table, graph_mode ? d->rope_cur : nullptr};
       void* no_y[3] = {nullptr, nullptr, nullptr};
-      if (lay) RC(strata_gemv_layout_run(lay[0], d->h, T, no_y, STRATA_BF16, &eq, stream));
+      if (lay) RC(layout_rows(lay[0], d->h, T, no_y, eq, Hq, Hkv, D, kv->Lmax, stream));
       else RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, qkv, 3, eq, stream));
       AttnExtra ex;
       ex.part = d->part;
@@ -153,18 +175,18 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
       strata_q4_weight o = Lw.o;
       o.y = d->h;
       void* yh[1] = {d->h};
-      if (lay) RC(strata_gemv_layout_run(lay[1], d->attn, T, yh, STRATA_BF16, &er, stream));
+      if (lay) RC(layout_rows(lay[1], d->attn, T, yh, er, Hq, Hkv, D, kv->Lmax, stream));
       else RC(strata_q4_gemv_epi(d->ctx, d->attn, T, Hq * D, &o, 1, er, stream));
       strata_q4_weight gu[2] = {Lw.gate, Lw.up};
       gu[0].y = d->act;
       GemvEpilogue es{1, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr, Lw.post_norm,
                       c.rms_norm_eps, nullptr};
       void* ya[1] = {d->act};
-      if (lay) RC(strata_gemv_layout_run(lay[2], d->h, T, ya, STRATA_BF16, &es, stream));
+      if (lay) RC(layout_rows(lay[2], d->h, T, ya, es, Hq, Hkv, D, kv->Lmax, stream));
       else RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, gu, 2, es, stream));
       strata_q4_weight dn = Lw.down;
       dn.y = d->h;
-      if (lay) RC(strata_gemv_layout_run(lay[3], d->act, T, yh, STRATA_BF16, &er, stream));
+      if (lay) RC(layout_rows(lay[3], d->act, T, yh, er, Hq, Hkv, D, kv->Lmax, stream));
       else RC(strata_q4_gemv_epi(d->ctx, d->act, T, F, &dn, 1, er, stream));
     }
     RC(strata_rmsnorm_launch(d->h, nullptr, d->final_norm, T, H, c.rms_norm_eps, d->hn, stream));

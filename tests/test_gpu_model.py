@@ -175,8 +175,10 @@ def test_engine_batched_heads_decode_on_mfma(dev):
     wave-private K/V rings.  Cache slots past the length hold NaN: the graph
     steps (device-held key count, 256-key bucket capacity) fetch whole 32-key
     tiles past the count, the host-launched steps do not.  Both must choose
-    the same tokens, and the op-by-op path (the same kernels driven from
-    Python) too.  The kernel itself is checked against float64 attention in
+    the same tokens.  The op-by-op path (Python-driven, the row-block GEMV
+    on the MLX layout where the engine runs the layout GEMV in two 4-row
+    launches) must give the same logits to the bf16 tolerance.  The kernel
+    itself is checked against float64 attention in
     test_gpu_attention.py::test_decode_batched_heads_mfma; token parity with
     the oracle is left to the smaller models above, whose top-2 logit margins
     exceed the bf16 flow's logit error at every step."""
@@ -190,6 +192,14 @@ def test_engine_batched_heads_decode_on_mfma(dev):
     got = eng.generate(prompt, 8).cpu()
     assert not torch.isnan(cache.k_storage[:, :, :, :97]).any()  # 90 prompt + 7 appended
     host = model.generate(prompt, max_new_tokens=8, use_graph=False).cpu()
-    ops_path = model.generate(prompt, max_new_tokens=8, engine=False).cpu()
     assert torch.equal(host, got)
-    assert torch.equal(ops_path, got)
+    # one decode step on both paths from the same prefix
+    seq = got[:, :91]
+    cache.clear()
+    eng.forward(seq[:, :90])
+    eng_logits = to_np_f32(eng.forward(seq[:, 90:91]))
+    c2 = model.new_cache(8, 128)
+    model(seq[:, :90], past_key_values=c2, use_cache=True, logits="last")
+    op_logits = to_np_f32(model(seq[:, 90:91], past_key_values=c2, use_cache=True,
+                                logits="last")[:, -1])
+    assert rel_err(eng_logits, op_logits) < 2e-2
