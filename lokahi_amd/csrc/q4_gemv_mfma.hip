@@ -208,16 +208,9 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
     }
   }
 
-
-  // stage x in the wave's own LDS region (no barrier: only this wave reads it)
-#pragma unroll
-  for (int m = 0; m < MM; ++m)
-#pragma unroll
-    for (int ee = 0; ee < NE; ++ee)
-      xw[m * 128 + lane + 64 * (HT == 2 ? hh : ee)] = m < M ? xv[m][ee] : make_uint4(0, 0, 0, 0);
   // RMSNorm prologue (llama_mlx.py:77-92): r = 1/sqrt(mean(x^2) + eps) over
   // the whole row (the block's waves together hold it), then
-  // x <- bf16(w * (x * r)) with each product rounded.
+  // x <- bf16(w * (x * r)) with each product rounded, in registers.
   if constexpr (NORM) {
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
@@ -243,9 +236,7 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
       const float r = 1.0f / sqrtf(tot / static_cast<float>(K) + a.eps);
 #pragma unroll
       for (int ee = 0; ee < NE; ++ee) {
-        const int e = HT == 2 ? hh : ee;
-        uint4 v = xw[m * 128 + lane + 64 * e];
-        uint32_t* u = reinterpret_cast<uint32_t*>(&v);
+        uint32_t* u = reinterpret_cast<uint32_t*>(&xv[m][ee]);
         const uint32_t wu[4] = {wn[ee].x, wn[ee].y, wn[ee].z, wn[ee].w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -254,17 +245,18 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
                                   __uint_as_float(wu[c] & 0xffff0000u));
           u[c] = static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
         }
-        xw[m * 128 + lane + 64 * e] = v;
       }
     }
   }
-  // group sums of the staged x
+  // stage x in the wave's own LDS region (no barrier: only this wave reads
+  // it) and take its group sums from the registers
 #pragma unroll
   for (int m = 0; m < MM; ++m)
 #pragma unroll
     for (int ee = 0; ee < NE; ++ee) {
       const int e = HT == 2 ? hh : ee;
-      const uint4 v = xw[m * 128 + lane + 64 * e];
+      const uint4 v = m < M ? xv[m][ee] : make_uint4(0, 0, 0, 0);
+      xw[m * 128 + lane + 64 * e] = v;
       const uint32_t u[4] = {v.x, v.y, v.z, v.w};
       float s = 0.f;
 #pragma unroll
