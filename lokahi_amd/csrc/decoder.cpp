@@ -104,13 +104,15 @@ int alloc(void** p, size_t bytes) {
 
 constexpr int kKeyBucket = 256;
 
-// The layout GEMV over T <= 8 rows: launches of at most 4 rows (its widest
-// batch tile), each with x, the outputs and the epilogue's per-row
-// destinations advanced to its first row.
+// The layout GEMV over T <= 8 rows: one launch when the layout's K takes 8
+// rows, else launches of at most 4 rows, each with x, the outputs and the
+// epilogue's per-row destinations advanced to its first row.
 int layout_rows(const GemvLayout& L, const void* x, int T, void* const* ys, const GemvEpilogue& e,
                 int Hq, int Hkv, int D, int lmax, void* stream) {
-  for (int r0 = 0; r0 < T; r0 += 4) {
-    const int m = std::min(4, T - r0);
+  // one launch of up to 8 rows where the layout's K allows it, else 4-row launches
+  const int per = strata_gemv_layout_fits(L.K, T) ? T : 4;
+  for (int r0 = 0; r0 < T; r0 += per) {
+    const int m = std::min(per, T - r0);
     void* y[kGvMaxProblems] = {};
     for (int i = 0; i < L.count; ++i)
       y[i] = ys[i] ? static_cast<uint16_t*>(ys[i]) + (int64_t)r0 * L.N[i] : nullptr;

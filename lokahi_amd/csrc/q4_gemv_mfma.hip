@@ -106,15 +106,16 @@ template <int MP, int EPI>
 constexpr int kGvWavesPerEu = MP != 0 ? 2 : (EPI == 2 ? 4 : 7);
 
 // NTC: the K task count when known at compile time (4: the 8B hidden width,
-// 14: the 8B FFN width, 3 and 8: the 3B widths), 0 for any (up to 16).
+// 14: the 8B FFN width, 3 and 8: the 3B widths), 0 for any (up to 16; up to
+// 8 for the 8-row kernels, MP 2).
 // HT: waves per K task.  With HT = 2 (batch 1, launches too small to fill
 // the GPU) each wave takes half a task, 4 of its 8 weight loads and 2 of its
 // 4 phases, so the block has twice the waves, each with half the chain.
 template <int MP, int EPI, bool NORM, typename YT, int NTC, int HT = 1>
-__global__ __launch_bounds__(NTC ? 64 * NTC * HT : 1024) __attribute__((amdgpu_waves_per_eu(kGvWavesPerEu<MP, EPI>)))
+__global__ __launch_bounds__(NTC ? 64 * NTC * HT : (MP == 2 ? 512 : 1024)) __attribute__((amdgpu_waves_per_eu(kGvWavesPerEu<MP, EPI>)))
 void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   static_assert(HT == 1 || (HT == 2 && MP == 0), "half tasks are batch-1 only");
-  constexpr int MM = MP == 0 ? 1 : 4;  // staged batch rows
+  constexpr int MM = MP == 0 ? 1 : 4 * MP;  // staged batch rows (MP 2: 8)
   constexpr int NE = 2 / HT;           // x uint4 per lane of the wave's (half) task
   constexpr int NWL = 8 / HT;          // weight loads per lane
   extern __shared__ uint4 smem[];
@@ -185,7 +186,9 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
     if (q < a.count && rb >= a.p[q].rb0) pi = q;
   const int lb = rb - a.p[pi].rb0;
   const int em = threadIdx.x >> 4, er = threadIdx.x & 15;  // epilogue thread: batch row, block row
-  const bool eth = wave == 0 && em < M;
+  // (MP 2: batch rows 4..7 on the second wave; the host launches it with at
+  // least two waves)
+  const bool eth = (MP == 2 ? wave < 2 : wave == 0) && em < M;
   // epilogue operands, fetched now (they return with the weights); the
   // residual values are loaded by every lane at an in-bounds index
   uint16_t hpre = 0;
@@ -326,40 +329,63 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
       for (int i = 0; i < 4; ++i) red[wave * 16 + 4 * j + i] = acc[i];
     }
   } else {
-    // column n = 4 b + j': batch row b, group 4 ph + j' of the phase
+    // column n = 4 b + j': batch row b (+ 4 hf for the second accumulator
+    // set of MP 2, which shares every A operand), group 4 ph + j' of the phase
+    constexpr int NH = MM / 4;
     const int bm = n >> 2, jg = n & 3;
-    const bool act = jg == j && bm < M;
+    float accs[NH][4];
+#pragma unroll
+    for (int hf = 0; hf < NH; ++hf)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) accs[hf][i] = 0.f;
 #pragma unroll
     for (int ph = 0; ph < 4; ++ph) {
-      const uint4* bb = act ? xw + bm * 128 + (4 * ph + j) * 8 : zero;
-      f32x4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+      const uint4* bb[NH];
+#pragma unroll
+      for (int hf = 0; hf < NH; ++hf)
+        bb[hf] = jg == j && 4 * hf + bm < M ? xw + (4 * hf + bm) * 128 + (4 * ph + j) * 8 : zero;
+      f32x4_t c0[NH], c1[NH];
+#pragma unroll
+      for (int hf = 0; hf < NH; ++hf) {
+        c0[hf] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        c1[hf] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
       for (int o = 0; o < 8; ++o) {
         const u32x4_t av = a_op(8 * ph + o);
-        const uint4 bv = bb[o];
-        const u32x4_t bq = {bv.x, bv.y, bv.z, bv.w};
-        if (o & 1) c1 = mfma16(av, bq, c1);
-        else c0 = mfma16(av, bq, c0);
+#pragma unroll
+        for (int hf = 0; hf < NH; ++hf) {
+          const uint4 bv = bb[hf][o];
+          const u32x4_t bq = {bv.x, bv.y, bv.z, bv.w};
+          if (o & 1) c1[hf] = mfma16(av, bq, c1[hf]);
+          else c0[hf] = mfma16(av, bq, c0[hf]);
+        }
       }
-      const float X = xs[min(bm, MM - 1) * 16 + 4 * ph + jg];
       const uint32_t sw[4] = {sbv[ph].x, sbv[ph].y, sbv[ph].z, sbv[ph].w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float sc = __uint_as_float(sw[i] << 16), bc = __uint_as_float(sw[i] & 0xffff0000u);
-        acc[i] += sc * (c0[i] + c1[i]) + fmaf(-128.f, sc, bc) * X;
+      for (int hf = 0; hf < NH; ++hf) {
+        const float X = xs[min(4 * hf + bm, MM - 1) * 16 + 4 * ph + jg];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float sc = __uint_as_float(sw[i] << 16), bc = __uint_as_float(sw[i] & 0xffff0000u);
+          accs[hf][i] += sc * (c0[hf][i] + c1[hf][i]) + fmaf(-128.f, sc, bc) * X;
+        }
       }
     }
     // sum the 4 group columns of each batch row (one lane quad)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float v = acc[i];
-      v += dppv<0xB1>(v);
-      v += dppv<0x4E>(v);
-      acc[i] = v;
-    }
-    if (jg == 0 && bm < M) {
+    for (int hf = 0; hf < NH; ++hf) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red[(wave * MM + bm) * 16 + 4 * j + i] = acc[i];
+      for (int i = 0; i < 4; ++i) {
+        float v = accs[hf][i];
+        v += dppv<0xB1>(v);
+        v += dppv<0x4E>(v);
+        accs[hf][i] = v;
+      }
+      if (jg == 0 && 4 * hf + bm < M) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[(wave * MM + 4 * hf + bm) * 16 + 4 * j + i] = accs[hf][i];
+      }
     }
   }
   __syncthreads();
@@ -514,7 +540,7 @@ constexpr int64_t kGvHalfTaskWaves = 4096;
 
 template <int MP, int EPI, bool NORM, typename YT, int NTC, int HT>
 void launch_one(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
-  constexpr int MM = MP == 0 ? 1 : 4;
+  constexpr int MM = MP == 0 ? 1 : 4 * MP;
   const int waves = a.nt * HT;
   const size_t lds = (size_t)waves * (kWaveLds<MM> + MM * 64 + MM * 4);
   hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, NTC, HT>), dim3(nrb), dim3(64 * waves),
@@ -529,21 +555,23 @@ void launch_gv(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
     else launch_one<MP, EPI, NORM, YT, 4, 1>(x, a, nrb, st);
     return;
   }
-  if (a.nt == 14 && !NORM) {
-    launch_one<MP, EPI, NORM, YT, 14, 1>(x, a, nrb, st);
+  if constexpr (MP != 2) {  // (8 staged rows of 14 tasks exceed the LDS)
+    if (a.nt == 14 && !NORM) {
+      launch_one<MP, EPI, NORM, YT, 14, 1>(x, a, nrb, st);
+      return;
+    }
+  }
+  // the 3B widths (3072, and 8192 for down); the batched kernels need the
+  // small block's register budget too (the generic 1024-thread bound spills)
+  if (a.nt == 3) {
+    if (half) launch_one<MP, EPI, NORM, YT, 3, MP == 0 ? 2 : 1>(x, a, nrb, st);
+    else launch_one<MP, EPI, NORM, YT, 3, 1>(x, a, nrb, st);
     return;
   }
-  if constexpr (MP == 0) {  // batch 1 at the 3B widths (3072, and 8192 for down)
-    if (a.nt == 3) {
-      if (half) launch_one<MP, EPI, NORM, YT, 3, 2>(x, a, nrb, st);
-      else launch_one<MP, EPI, NORM, YT, 3, 1>(x, a, nrb, st);
-      return;
-    }
-    if (a.nt == 8 && !NORM) {
-      if (half) launch_one<MP, EPI, NORM, YT, 8, 2>(x, a, nrb, st);
-      else launch_one<MP, EPI, NORM, YT, 8, 1>(x, a, nrb, st);
-      return;
-    }
+  if (a.nt == 8 && !NORM) {
+    if (half) launch_one<MP, EPI, NORM, YT, 8, MP == 0 ? 2 : 1>(x, a, nrb, st);
+    else launch_one<MP, EPI, NORM, YT, 8, 1>(x, a, nrb, st);
+    return;
   }
   launch_one<MP, EPI, NORM, YT, 0, 1>(x, a, nrb, st);
 }
@@ -551,13 +579,15 @@ void launch_gv(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
 template <int EPI, bool NORM, typename YT>
 void launch_gv_m(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
   if (a.M == 1) launch_gv<0, EPI, NORM, YT>(x, a, nrb, st);
-  else launch_gv<1, EPI, NORM, YT>(x, a, nrb, st);
+  else if (a.M <= 4) launch_gv<1, EPI, NORM, YT>(x, a, nrb, st);
+  else launch_gv<2, EPI, NORM, YT>(x, a, nrb, st);
 }
 
 }  // namespace
 
 bool strata_gemv_layout_fits(int K, int M) {
-  return K > 0 && K % 64 == 0 && K <= 16384 && M >= 1 && M <= 4;
+  return K > 0 && K % 64 == 0 && K <= 16384 && M >= 1 &&
+         (M <= 4 || (M <= kGvMaxRows && gv_eight_rows(K)));
 }
 
 int strata_gemv_layout_build(const strata_q4_weight* ws, int count, int K, int perm, int head_dim,
@@ -633,7 +663,8 @@ void strata_gemv_layout_free(GemvLayout* L) {
 int strata_gemv_layout_run(const GemvLayout& L, const void* x, int M, void* const* ys, int y_dtype,
                            const GemvEpilogue* e, void* stream) {
   STRATA_REQUIRE(L.buf != nullptr, "GEMV layout: not built");
-  STRATA_REQUIRE(M >= 1 && M <= 4, "GEMV layout: M=%d outside 1..4", M);
+  STRATA_REQUIRE(M >= 1 && (M <= 4 || (M <= kGvMaxRows && gv_eight_rows(L.K))),
+                 "GEMV layout: M=%d outside 1..4 (1..8 for 1024 < K <= 8192)", M);
   STRATA_REQUIRE(x != nullptr && ys != nullptr, "GEMV layout: null x/y");
   GvArgs a{};
   a.codes = static_cast<const uint4*>(L.buf);

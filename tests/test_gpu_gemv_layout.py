@@ -59,6 +59,42 @@ def test_layout_gemv_batches_ragged_rows_padded_k(dev, M):
         assert rel_err(to_np_f32(y), q4.quantized_matmul(bf16_bits_to_f32(x), w, s, b)) < TOL_F32
 
 
+@pytest.mark.parametrize("M,K", [(5, 1088), (8, 3072), (6, 4096), (7, 8192), (8, 4096)])
+def test_layout_gemv_eight_rows_equal_two_four_row_calls(dev, M, K):
+    """5..8 rows run one launch that reads each weight block once and feeds
+    two 4-row accumulator sets from the same A operands: every row is
+    bit-identical to the same row in a 4-row call, and within the fp32
+    tolerance of the oracle."""
+    rng = np.random.default_rng(50 + M + K)
+    probs = [_weights(rng, n, K) for n in (100, 36, 17)]
+    lay = _layout(dev, probs)
+    x = _x(rng, M, K)
+    tx = to_dev(x, dev)
+    ys = lay(tx, out_dtype=torch.float32)
+    lo = lay(tx[:4].contiguous(), out_dtype=torch.float32)
+    # rows M-4 .. M-1 (a 4-row call: a single row would take the 1-row kernel)
+    hi = lay(tx[M - 4:].contiguous(), out_dtype=torch.float32)
+    ys16 = lay(tx)
+    for (w, s, b), y, a, c, y16 in zip(probs, ys, lo, hi, ys16):
+        assert y.shape == (M, w.shape[0])
+        assert torch.equal(y[:4], a) and torch.equal(y[4:], c[8 - M:])
+        ref = q4.quantized_matmul(bf16_bits_to_f32(x), w, s, b)
+        assert rel_err(to_np_f32(y), ref) < TOL_F32
+        assert rel_err(to_np_f32(y16), ref) < TOL_BF16
+
+
+def test_layout_gemv_rejects_eight_rows_outside_its_k_range(dev):
+    rng = np.random.default_rng(58)
+    for K in (1024, 9216):
+        lay = _layout(dev, [_weights(rng, 32, K)])
+        with pytest.raises(ValueError, match="K"):
+            lay(to_dev(_x(rng, 5, K), dev))
+        lay(to_dev(_x(rng, 4, K), dev))  # 4 rows take any K
+    lay = _layout(dev, [_weights(rng, 32, 2048)])
+    with pytest.raises(ValueError, match="outside"):
+        lay(to_dev(_x(rng, 9, 2048), dev))
+
+
 def test_layout_gemv_matches_mlx_layout_gemv(dev):
     from lokahi_amd import ops
     rng = np.random.default_rng(41)

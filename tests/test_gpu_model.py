@@ -177,7 +177,8 @@ def test_engine_batched_heads_decode_on_mfma(dev):
     tiles past the count, the host-launched steps do not.  Both must choose
     the same tokens.  The op-by-op path (Python-driven, the row-block GEMV
     on the MLX layout where the engine runs the layout GEMV in two 4-row
-    launches) must give the same logits to the bf16 tolerance.  The kernel
+    launches at this 1024-wide K) must give the same logits to the bf16
+    tolerance.  The kernel
     itself is checked against float64 attention in
     test_gpu_attention.py::test_decode_batched_heads_mfma; token parity with
     the oracle is left to the smaller models above, whose top-2 logit margins
@@ -201,5 +202,35 @@ def test_engine_batched_heads_decode_on_mfma(dev):
     c2 = model.new_cache(8, 128)
     model(seq[:, :90], past_key_values=c2, use_cache=True, logits="last")
     op_logits = to_np_f32(model(seq[:, 90:91], past_key_values=c2, use_cache=True,
+                                logits="last")[:, -1])
+    assert rel_err(eng_logits, op_logits) < 2e-2
+
+
+EIGHT_ROWS = oll.Config(vocab_size=256, hidden_size=2048, intermediate_size=3072,
+                        num_hidden_layers=2, num_attention_heads=16, num_key_value_heads=8,
+                        rms_norm_eps=1e-5, rope_theta=500000.0)
+
+
+def test_engine_eight_row_decode_one_layout_launch(dev):
+    """At K = 2048 and 3072 the engine's 8-row decode steps run each layout
+    GEMV (RMSNorm + RoPE + KV append, residual, RMSNorm + SiLU epilogues) as
+    one 8-row launch.  Graph-replayed and host-launched steps choose the same
+    tokens, and one step's logits match the op-by-op path (row-block GEMV on
+    the MLX layout) to the bf16 tolerance."""
+    from lokahi_amd.llama import DecoderEngine
+    model, _ = _pair(EIGHT_ROWS, seed=71, std=0.05)
+    prompt = torch.from_numpy(np.random.default_rng(71).integers(0, EIGHT_ROWS.vocab_size, (8, 40)))
+    cache = model.new_cache(8, 128)
+    eng = DecoderEngine(model, cache, max_batch=8, max_tokens=8 * 40)
+    got = eng.generate(prompt, 6).cpu()
+    host = model.generate(prompt, max_new_tokens=6, use_graph=False).cpu()
+    assert torch.equal(host, got)
+    seq = got[:, :41]
+    cache.clear()
+    eng.forward(seq[:, :40])
+    eng_logits = to_np_f32(eng.forward(seq[:, 40:41]))
+    c2 = model.new_cache(8, 64)
+    model(seq[:, :40], past_key_values=c2, use_cache=True, logits="last")
+    op_logits = to_np_f32(model(seq[:, 40:41], past_key_values=c2, use_cache=True,
                                 logits="last")[:, -1])
     assert rel_err(eng_logits, op_logits) < 2e-2
