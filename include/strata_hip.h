@@ -101,9 +101,8 @@ int strata_linear_q4_multi(strata_ctx* ctx, const void* x, int x_dtype, int64_t 
  * matrix-core decode GEMV streams (16-row blocks, scale and bias packed next
  * to the codes, K padded to a multiple of 1024); the MLX tensors may be
  * freed afterwards.  strata_linear_q4_layout then computes
- * y_i = x @ (scales_i*q_i + biases_i).T for 1 <= M <= 4 bf16 rows (up to 8
- * when 1024 < K <= 8192), fp32 accumulate, y_dtype f32 or bf16 (ys[i] is
- * [M, N_i]).
+ * y_i = x @ (scales_i*q_i + biases_i).T for 1 <= M <= 8 bf16 rows, fp32
+ * accumulate, y_dtype f32 or bf16 (ys[i] is [M, N_i]).
  * Requirements: K % 64 == 0, K <= 16384, count 1..8, group_size 64, 4 bits.
  * The layout is read-only after creation: calls may share it. */
 typedef struct strata_q4_layout strata_q4_layout;

@@ -76,7 +76,7 @@ namespace {
 int lm_head_launch(strata_decoder* d, const void* x, int M, float* logits, void* stream) {
   const strata_llama_config& c = d->cfg;
   if (d->head_q4.w) {
-    if (d->head_lay.buf && M <= 4) {
+    if (d->head_lay.buf && M <= kGvMaxRows) {
       void* ys[1] = {logits};
       return strata_gemv_layout_run(d->head_lay, x, M, ys, STRATA_F32, nullptr, stream);
     }
@@ -103,30 +103,6 @@ int alloc(void** p, size_t bytes) {
   } while (0)
 
 constexpr int kKeyBucket = 256;
-
-// The layout GEMV over T <= 8 rows: one launch when the layout's K takes 8
-// rows, else launches of at most 4 rows, each with x, the outputs and the
-// epilogue's per-row destinations advanced to its first row.
-int layout_rows(const GemvLayout& L, const void* x, int T, void* const* ys, const GemvEpilogue& e,
-                int Hq, int Hkv, int D, int lmax, void* stream) {
-  // one launch of up to 8 rows where the layout's K allows it, else 4-row launches
-  const int per = strata_gemv_layout_fits(L.K, T) ? T : 4;
-  for (int r0 = 0; r0 < T; r0 += per) {
-    const int m = std::min(per, T - r0);
-    void* y[kGvMaxProblems] = {};
-    for (int i = 0; i < L.count; ++i)
-      y[i] = ys[i] ? static_cast<uint16_t*>(ys[i]) + (int64_t)r0 * L.N[i] : nullptr;
-    GemvEpilogue er = e;
-    if (e.mode == 2 && r0 > 0) {  // q rows [B, Hq, 1, D], cache rows [B, Hkv, lmax, D]
-      er.q_out = e.q_out + (int64_t)r0 * Hq * D;
-      er.kc = e.kc + (int64_t)r0 * Hkv * lmax * D;
-      er.vc = e.vc + (int64_t)r0 * Hkv * lmax * D;
-    }
-    RC(strata_gemv_layout_run(L, static_cast<const uint16_t*>(x) + (int64_t)r0 * L.K, m, y,
-                              STRATA_BF16, &er, stream));
-  }
-  return STRATA_OK;
-}
 
 // One decoder forward over T = B*L tokens at positions pos0..pos0+L-1
 // (pos0 < 0: read from counters[1], decode graph mode, L == 1, with at most
@@ -162,7 +138,7 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
                       (uint16_t*)d->qr, (uint16_t*)kc, (uint16_t*)vc, Lw.input_norm,
                       c.rms_norm_eps, d->rope_table, graph_mode ? d->rope_cur : nullptr};
       void* no_y[3] = {nullptr, nullptr, nullptr};
-      if (lay) RC(layout_rows(lay[0], d->h, T, no_y, eq, Hq, Hkv, D, kv->Lmax, stream));
+      if (lay) RC(strata_gemv_layout_run(lay[0], d->h, T, no_y, STRATA_BF16, &eq, stream));
       else RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, qkv, 3, eq, stream));
       AttnExtra ex;
       ex.part = d->part;
@@ -177,18 +153,18 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
       strata_q4_weight o = Lw.o;
       o.y = d->h;
       void* yh[1] = {d->h};
-      if (lay) RC(layout_rows(lay[1], d->attn, T, yh, er, Hq, Hkv, D, kv->Lmax, stream));
+      if (lay) RC(strata_gemv_layout_run(lay[1], d->attn, T, yh, STRATA_BF16, &er, stream));
       else RC(strata_q4_gemv_epi(d->ctx, d->attn, T, Hq * D, &o, 1, er, stream));
       strata_q4_weight gu[2] = {Lw.gate, Lw.up};
       gu[0].y = d->act;
       GemvEpilogue es{1, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr, Lw.post_norm,
                       c.rms_norm_eps, nullptr};
       void* ya[1] = {d->act};
-      if (lay) RC(layout_rows(lay[2], d->h, T, ya, es, Hq, Hkv, D, kv->Lmax, stream));
+      if (lay) RC(strata_gemv_layout_run(lay[2], d->h, T, ya, STRATA_BF16, &es, stream));
       else RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, gu, 2, es, stream));
       strata_q4_weight dn = Lw.down;
       dn.y = d->h;
-      if (lay) RC(layout_rows(lay[3], d->act, T, yh, er, Hq, Hkv, D, kv->Lmax, stream));
+      if (lay) RC(strata_gemv_layout_run(lay[3], d->act, T, yh, STRATA_BF16, &er, stream));
       else RC(strata_q4_gemv_epi(d->ctx, d->act, T, F, &dn, 1, er, stream));
     }
     RC(strata_rmsnorm_launch(d->h, nullptr, d->final_norm, T, H, c.rms_norm_eps, d->hn, stream));

@@ -80,6 +80,8 @@ struct GvArgs {
   int count;
   GvProblem p[kGvMaxProblems];
   int rb_end[kGvMaxProblems];
+  int nrb;   // row blocks of the layout
+  int pair;  // MP 1, 5-8 rows: both 4-row halves of every row block in one grid
   // RoPE / KV append (EPI_ROPE)
   int head_dim, n_heads, n_kv_heads, lmax, pos0;
   const int* dpos;            // device position (graph-replayed step) or null
@@ -119,16 +121,29 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   constexpr int NE = 2 / HT;           // x uint4 per lane of the wave's (half) task
   constexpr int NWL = 8 / HT;          // weight loads per lane
   extern __shared__ uint4 smem[];
-  const int nt = NTC ? NTC : a.nt, M = a.M, K = a.K;
+  const int nt = NTC ? NTC : a.nt, K = a.K;
+  // a.pair (MP 1, 5-8 rows): workgroups 16 i + c and 16 i + 8 + c take batch
+  // rows 0-3 and 4-7 of row block 8 i + c.  Both run on XCD c, one soon
+  // after the other, so the second finds the block's weights in that L2.
+  int rb = blockIdx.x, ro = 0;
+  if constexpr (MP == 1) {
+    if (a.pair) {
+      const int slot = rb >> 3;
+      ro = 4 * (slot & 1);
+      rb = (slot >> 1) * 8 + (rb & 7);
+      if (rb >= a.nrb) return;  // grid padding (whole workgroup)
+    }
+  }
+  const int M = MP == 1 ? min(4, a.M - ro) : a.M;  // rows of this workgroup
+  const uint16_t* const xp = x + (int64_t)ro * K;
   // Every kernel argument the load issue below needs, in SGPRs at once: one
   // wait for the argument loads instead of one per field between the loads.
   const uint4* const codes = a.codes;
   const uint4* const sbp = a.sb;
   const uint16_t* const nw = NORM ? a.norm_w : nullptr;
-  asm volatile("" ::"s"(x), "s"(codes), "s"(sbp), "s"(nw), "s"(M), "s"(K), "s"(nt));
+  asm volatile("" ::"s"(xp), "s"(codes), "s"(sbp), "s"(nw), "s"(M), "s"(K), "s"(nt));
   const int lane = threadIdx.x & 63, j = lane >> 4, n = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rb = blockIdx.x;
   const int t = HT == 2 ? wave >> 1 : wave;  // this wave's K task
   const int hh = HT == 2 ? wave & 1 : 0;     // and its half (HT = 2)
   const int nw_ = nt * HT;                   // waves of the block
@@ -149,7 +164,7 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
       const int e = HT == 2 ? hh : ee;
       const int k = 1024 * t + 8 * (lane + 64 * e);
       const int mc = min(m, M - 1);
-      xv[m][ee] = k < K ? *reinterpret_cast<const uint4*>(x + (int64_t)mc * K + k)
+      xv[m][ee] = k < K ? *reinterpret_cast<const uint4*>(xp + (int64_t)mc * K + k)
                         : make_uint4(0, 0, 0, 0);
     }
   if constexpr (NORM) {
@@ -186,6 +201,7 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
     if (q < a.count && rb >= a.p[q].rb0) pi = q;
   const int lb = rb - a.p[pi].rb0;
   const int em = threadIdx.x >> 4, er = threadIdx.x & 15;  // epilogue thread: batch row, block row
+  const int eb = em + ro;  // its row of the whole batch
   // (MP 2: batch rows 4..7 on the second wave; the host launches it with at
   // least two waves)
   const bool eth = (MP == 2 ? wave < 2 : wave == 0) && em < M;
@@ -194,7 +210,7 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
   uint16_t hpre = 0;
   if constexpr (EPI == GV_RESID) {
     const int64_t nl = min(16 * (int64_t)lb + er, a.p[pi].n - 1);
-    hpre = reinterpret_cast<const uint16_t*>(a.p[pi].y)[(int64_t)min(em, M - 1) * a.p[pi].n + nl];
+    hpre = reinterpret_cast<const uint16_t*>(a.p[pi].y)[(int64_t)(min(em, M - 1) + ro) * a.p[pi].n + nl];
   }
   int pos = a.pos0;
   float2 cs = make_float2(0.f, 0.f);
@@ -402,10 +418,10 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
     if (nl >= P.n) return;
     const float v = total(er);
     if constexpr (EPI == GV_RESID) {
-      uint16_t* hp = reinterpret_cast<uint16_t*>(P.y) + (int64_t)em * P.n + nl;
+      uint16_t* hp = reinterpret_cast<uint16_t*>(P.y) + (int64_t)eb * P.n + nl;
       *hp = f32_to_bf16(bf16_to_f32(hpre) + bf16_to_f32(f32_to_bf16(v)));
     } else {
-      Elem<YT>::store(reinterpret_cast<YT*>(P.y), (int64_t)em * P.n + nl, v);
+      Elem<YT>::store(reinterpret_cast<YT*>(P.y), (int64_t)eb * P.n + nl, v);
     }
   } else if constexpr (EPI == GV_SILU) {
     // act = bf16(silu(bf16(gate)) * bf16(up))   (llama_mlx.py:399-407)
@@ -414,7 +430,7 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
     const float g = bf16_to_f32(f32_to_bf16(total(er)));
     const float u = bf16_to_f32(f32_to_bf16(total(er + 8)));
     const float sg = g / (1.0f + expf(-g));
-    reinterpret_cast<uint16_t*>(P.y)[(int64_t)em * P.n + nl] = f32_to_bf16(mul_rn(sg, u));
+    reinterpret_cast<uint16_t*>(P.y)[(int64_t)eb * P.n + nl] = f32_to_bf16(mul_rn(sg, u));
   } else {
     // q/k/v: RoPE on q and k at the step's position, k and v into the cache
     // (llama_mlx.py:271-297; values rounded to bf16 before the rotation)
@@ -424,18 +440,18 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
     const float a0 = bf16_to_f32(f32_to_bf16(total(er)));
     const float a1 = bf16_to_f32(f32_to_bf16(total(er + 8)));
     if (pi == 2) {
-      const int64_t co = (((int64_t)em * a.n_kv_heads + h) * a.lmax + pos) * D;
+      const int64_t co = (((int64_t)eb * a.n_kv_heads + h) * a.lmax + pos) * D;
       a.vc[co + i] = f32_to_bf16(a0);
       a.vc[co + i + half] = f32_to_bf16(a1);
     } else {
       float o1, o2;
       rotate_pair(a0, a1, cs.x, cs.y, &o1, &o2);
       if (pi == 0) {
-        const int64_t qo = ((int64_t)em * a.n_heads + h) * D;
+        const int64_t qo = ((int64_t)eb * a.n_heads + h) * D;
         a.q_out[qo + i] = f32_to_bf16(o1);
         a.q_out[qo + i + half] = f32_to_bf16(o2);
       } else {
-        const int64_t co = (((int64_t)em * a.n_kv_heads + h) * a.lmax + pos) * D;
+        const int64_t co = (((int64_t)eb * a.n_kv_heads + h) * a.lmax + pos) * D;
         a.kc[co + i] = f32_to_bf16(o1);
         a.kc[co + i + half] = f32_to_bf16(o2);
       }
@@ -543,7 +559,8 @@ void launch_one(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
   constexpr int MM = MP == 0 ? 1 : 4 * MP;
   const int waves = a.nt * HT;
   const size_t lds = (size_t)waves * (kWaveLds<MM> + MM * 64 + MM * 4);
-  hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, NTC, HT>), dim3(nrb), dim3(64 * waves),
+  const int grid = a.pair ? 2 * ((nrb + 7) / 8 * 8) : nrb;
+  hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, NTC, HT>), dim3(grid), dim3(64 * waves),
                      lds, st, x, a);
 }
 
@@ -578,16 +595,23 @@ void launch_gv(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
 
 template <int EPI, bool NORM, typename YT>
 void launch_gv_m(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
-  if (a.M == 1) launch_gv<0, EPI, NORM, YT>(x, a, nrb, st);
-  else if (a.M <= 4) launch_gv<1, EPI, NORM, YT>(x, a, nrb, st);
-  else launch_gv<2, EPI, NORM, YT>(x, a, nrb, st);
+  if (a.M == 1) {
+    launch_gv<0, EPI, NORM, YT>(x, a, nrb, st);
+  } else if (a.M <= 4) {
+    launch_gv<1, EPI, NORM, YT>(x, a, nrb, st);
+  } else if (gv_eight_rows(a.K)) {
+    launch_gv<2, EPI, NORM, YT>(x, a, nrb, st);
+  } else {  // 8 staged rows would not fit the LDS: paired 4-row workgroups
+    GvArgs b = a;
+    b.pair = 1;
+    launch_gv<1, EPI, NORM, YT>(x, b, nrb, st);
+  }
 }
 
 }  // namespace
 
 bool strata_gemv_layout_fits(int K, int M) {
-  return K > 0 && K % 64 == 0 && K <= 16384 && M >= 1 &&
-         (M <= 4 || (M <= kGvMaxRows && gv_eight_rows(K)));
+  return K > 0 && K % 64 == 0 && K <= 16384 && M >= 1 && M <= kGvMaxRows;
 }
 
 int strata_gemv_layout_build(const strata_q4_weight* ws, int count, int K, int perm, int head_dim,
@@ -663,8 +687,7 @@ void strata_gemv_layout_free(GemvLayout* L) {
 int strata_gemv_layout_run(const GemvLayout& L, const void* x, int M, void* const* ys, int y_dtype,
                            const GemvEpilogue* e, void* stream) {
   STRATA_REQUIRE(L.buf != nullptr, "GEMV layout: not built");
-  STRATA_REQUIRE(M >= 1 && (M <= 4 || (M <= kGvMaxRows && gv_eight_rows(L.K))),
-                 "GEMV layout: M=%d outside 1..4 (1..8 for 1024 < K <= 8192)", M);
+  STRATA_REQUIRE(M >= 1 && M <= kGvMaxRows, "GEMV layout: M=%d outside 1..%d", M, kGvMaxRows);
   STRATA_REQUIRE(x != nullptr && ys != nullptr, "GEMV layout: null x/y");
   GvArgs a{};
   a.codes = static_cast<const uint4*>(L.buf);
@@ -672,6 +695,7 @@ int strata_gemv_layout_run(const GemvLayout& L, const void* x, int M, void* cons
   a.M = M;
   a.K = L.K;
   a.nt = L.nt;
+  a.nrb = L.nrb;
   a.count = L.count;
   for (int i = 0; i < L.count; ++i) {
     a.p[i].y = ys[i];

@@ -130,8 +130,8 @@ class Q4Layout:
     """Linears sharing ``x`` copied once into the decode GEMV's load-time
     layout (``strata_q4_layout_create``; the reference's load step is
     ``_load_layer_weights``, ``src/ollm/llama_mlx.py:550-580``).  Calling it
-    runs ``_linear`` on each of them (``llama_mlx.py:53-74``) for 1..4 bf16
-    rows of ``x`` (1..8 when 1024 < K <= 8192) on the matrix-core GEMV."""
+    runs ``_linear`` on each of them (``llama_mlx.py:53-74``) for 1..8 bf16
+    rows of ``x`` on the matrix-core GEMV."""
 
     def __init__(self, weights: Sequence[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]],
                  *, group_size: int = 64, bits: int = 4):
