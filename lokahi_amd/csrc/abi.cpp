@@ -103,8 +103,8 @@ int strata_ctx_create(int device, strata_ctx** out) {
 
 int strata_ctx_destroy(strata_ctx* ctx) {
   if (!ctx) return STRATA_OK;
-  hipDeviceSynchronize();
-  if (ctx->scratch) hipFree(ctx->scratch);
+  (void)hipDeviceSynchronize();
+  if (ctx->scratch) (void)hipFree(ctx->scratch);
   delete ctx;
   return STRATA_OK;
 }
@@ -315,7 +315,7 @@ int strata_kv_create(strata_ctx* ctx, int layers, int B, int Hkv, int Lmax, int 
       return strata_set_error(STRATA_ENOMEM, "KV cache allocation of %zu bytes failed", bytes);
     }
     if (hipMalloc(&kv->v, bytes) != hipSuccess) {
-      hipFree(kv->k);
+      (void)hipFree(kv->k);
       delete kv;
       return strata_set_error(STRATA_ENOMEM, "KV cache allocation of %zu bytes failed", bytes);
     }
@@ -328,9 +328,9 @@ int strata_kv_create(strata_ctx* ctx, int layers, int B, int Hkv, int Lmax, int 
 int strata_kv_destroy(strata_kv* kv) {
   if (!kv) return STRATA_OK;
   if (kv->owned) {
-    hipDeviceSynchronize();
-    hipFree(kv->k);
-    hipFree(kv->v);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(kv->k);
+    (void)hipFree(kv->v);
   }
   delete kv;
   return STRATA_OK;
@@ -533,12 +533,15 @@ int strata_selftest(strata_ctx* ctx, char* json, size_t cap) {
   if (hipMalloc(&dw, w.size() * 4) == hipSuccess && hipMalloc(&ds, s.size() * 2) == hipSuccess &&
       hipMalloc(&db, b.size() * 2) == hipSuccess && hipMalloc(&dx, x.size() * 2) == hipSuccess &&
       hipMalloc(&dy, N * 4) == hipSuccess) {
-    hipMemcpy(dw, w.data(), w.size() * 4, hipMemcpyHostToDevice);
-    hipMemcpy(ds, s.data(), s.size() * 2, hipMemcpyHostToDevice);
-    hipMemcpy(db, b.data(), b.size() * 2, hipMemcpyHostToDevice);
-    hipMemcpy(dx, x.data(), x.size() * 2, hipMemcpyHostToDevice);
-    rc = strata_linear_q4(ctx, dx, STRATA_BF16, 1, K, (const uint32_t*)dw, (const uint16_t*)ds,
-                          (const uint16_t*)db, N, G, 4, dy, STRATA_F32, nullptr);
+    const bool copied =
+        hipMemcpy(dw, w.data(), w.size() * 4, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy(ds, s.data(), s.size() * 2, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy(db, b.data(), b.size() * 2, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy(dx, x.data(), x.size() * 2, hipMemcpyHostToDevice) == hipSuccess;
+    rc = copied ? strata_linear_q4(ctx, dx, STRATA_BF16, 1, K, (const uint32_t*)dw,
+                                   (const uint16_t*)ds, (const uint16_t*)db, N, G, 4, dy,
+                                   STRATA_F32, nullptr)
+                : strata_set_error(STRATA_EHIP, "selftest: host-to-device copy failed");
     if (rc == STRATA_OK && hipDeviceSynchronize() == hipSuccess &&
         hipMemcpy(y.data(), dy, N * 4, hipMemcpyDeviceToHost) == hipSuccess) {
       max_err = 0.f;
@@ -546,7 +549,8 @@ int strata_selftest(strata_ctx* ctx, char* json, size_t cap) {
       ok = max_err <= 1e-4f;
     }
   }
-  hipFree(dw); hipFree(ds); hipFree(db); hipFree(dx); hipFree(dy);
+  for (void* p : {dw, ds, db, dx, dy})
+    if (p) (void)hipFree(p);
   snprintf(json, cap,
            "{\"schema_version\":1,\"backend\":\"hip\",\"operation\":\"linear_q4_gemv\","
            "\"device\":%d,\"compute_units\":%d,\"dispatch_success\":%s,"

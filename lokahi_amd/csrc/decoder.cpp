@@ -148,8 +148,8 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
                                    kv_bs, kv_hs, nullptr, B, Hq, Hkv, 1,
                                    graph_mode ? key_cap : pos0 + 1, D, 1, 1e-12f, d->attn, ex,
                                    stream));
-      GemvEpilogue er{3, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr, nullptr, 0.f,
-                      nullptr};
+      GemvEpilogue er{};
+      er.mode = 3;
       strata_q4_weight o = Lw.o;
       o.y = d->h;
       void* yh[1] = {d->h};
@@ -157,8 +157,10 @@ int forward_layers(strata_decoder* d, int B, int L, int pos0, void* stream, int 
       else RC(strata_q4_gemv_epi(d->ctx, d->attn, T, Hq * D, &o, 1, er, stream));
       strata_q4_weight gu[2] = {Lw.gate, Lw.up};
       gu[0].y = d->act;
-      GemvEpilogue es{1, 0, 0, 0, 0, 0, nullptr, 0.f, nullptr, nullptr, nullptr, Lw.post_norm,
-                      c.rms_norm_eps, nullptr};
+      GemvEpilogue es{};
+      es.mode = 1;
+      es.norm_w = Lw.post_norm;
+      es.eps = c.rms_norm_eps;
       void* ya[1] = {d->act};
       if (lay) RC(strata_gemv_layout_run(lay[2], d->h, T, ya, STRATA_BF16, &es, stream));
       else RC(strata_q4_gemv_epi(d->ctx, d->h, T, H, gu, 2, es, stream));
@@ -406,8 +408,8 @@ int strata_decoder_create(strata_ctx* ctx, const strata_llama_config* cfg,
 
 int strata_decoder_destroy(strata_decoder* d) {
   if (!d) return STRATA_OK;
-  hipDeviceSynchronize();
-  for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
+  (void)hipDeviceSynchronize();
+  for (auto& kvp : d->graphs) (void)hipGraphExecDestroy(kvp.second);
   for (GemmPacked& p : d->packed) (void)hipFree(const_cast<void*>(p.buf));
   for (GemvLayout& L : d->dlay) strata_gemv_layout_free(&L);
   strata_gemv_layout_free(&d->head_lay);
@@ -415,8 +417,8 @@ int strata_decoder_destroy(strata_decoder* d) {
                   d->delta, d->hn, d->logits, d->ids, d->tokens, d->counters, d->part, d->amax,
                   d->rope_table, d->rope_cur};
   for (void* p : ptrs)
-    if (p) hipFree(p);
-  if (d->stream) hipStreamDestroy(d->stream);
+    if (p) (void)hipFree(p);
+  if (d->stream) (void)hipStreamDestroy(d->stream);
   delete d;
   return STRATA_OK;
 }
@@ -429,7 +431,7 @@ int strata_decoder_set_lm_head_q4(strata_decoder* d, const strata_q4_weight* hea
   STRATA_REQUIRE(aligned16(head->w), "set_lm_head_q4: packed weights must be 16-byte aligned");
   // captured decode steps hold the previous head
   STRATA_HIP_CHECK(hipStreamSynchronize(d->stream));
-  for (auto& kvp : d->graphs) hipGraphExecDestroy(kvp.second);
+  for (auto& kvp : d->graphs) (void)hipGraphExecDestroy(kvp.second);
   d->graphs.clear();
   strata_gemv_layout_free(&d->head_lay);
   d->head_q4 = *head;
@@ -472,7 +474,7 @@ int strata_decoder_generate(strata_decoder* d, const int32_t* prompt, int B, int
   hipEvent_t ev;
   STRATA_HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
   if (hipEventRecord(ev, as_stream(stream)) != hipSuccess || hipStreamWaitEvent(s, ev, 0) != hipSuccess) {
-    hipEventDestroy(ev);
+    (void)hipEventDestroy(ev);
     return strata_set_error(STRATA_EHIP, "generate: ordering after the caller's stream failed");
   }
   // Positions whose K/V the launched work appends; on any error the cache
@@ -527,13 +529,13 @@ int strata_decoder_generate(strata_decoder* d, const int32_t* prompt, int B, int
         const int crc = decode_step(s, cap);
         const hipError_t ce = hipStreamEndCapture(s, &g);
         if (crc || ce != hipSuccess) {
-          if (ce == hipSuccess && g) hipGraphDestroy(g);
+          if (ce == hipSuccess && g) (void)hipGraphDestroy(g);
           if (crc) return crc;
           return strata_set_error(STRATA_EHIP, "decode graph capture failed: %s",
                                   hipGetErrorString(ce));
         }
         const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-        hipGraphDestroy(g);
+        (void)hipGraphDestroy(g);
         if (ie != hipSuccess)
           return strata_set_error(STRATA_EHIP, "decode graph instantiation failed: %s",
                                   hipGetErrorString(ie));
@@ -552,7 +554,7 @@ int strata_decoder_generate(strata_decoder* d, const int32_t* prompt, int B, int
   const hipError_t e1 = hipEventRecord(ev, s);
   const hipError_t e2 = e1 == hipSuccess ? hipStreamWaitEvent(as_stream(stream), ev, 0) : e1;
   const hipError_t e3 = hipStreamSynchronize(s);
-  hipEventDestroy(ev);
+  (void)hipEventDestroy(ev);
   set_lengths(d, appended);
   if (rc) return rc;
   if (e2 != hipSuccess || e3 != hipSuccess)

@@ -70,18 +70,6 @@ __device__ __forceinline__ float ubyte(uint32_t v) {
   return r;
 }
 
-// 8 codes of one word -> 8 bf16 (s*q + b, fp32 FMA then RNE), k order.
-__device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float b) {
-  const uint32_t lo = w & 0x0f0f0f0fu;         // codes 0, 2, 4, 6
-  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;  // codes 1, 3, 5, 7
-  uint4 o;
-  o.x = pk_bf16(fmaf(s, ubyte<0>(lo), b), fmaf(s, ubyte<0>(hi), b));
-  o.y = pk_bf16(fmaf(s, ubyte<1>(lo), b), fmaf(s, ubyte<1>(hi), b));
-  o.z = pk_bf16(fmaf(s, ubyte<2>(lo), b), fmaf(s, ubyte<2>(hi), b));
-  o.w = pk_bf16(fmaf(s, ubyte<3>(lo), b), fmaf(s, ubyte<3>(hi), b));
-  return o;
-}
-
 // Tile index -> (m tile, n tile): groups of kGroupM M tiles sweeping the
 // N tiles.
 __device__ __forceinline__ void group_tile(int t, int mt, int nt, int* tm, int* tn) {
