@@ -27,6 +27,9 @@ COMMON = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # packed-FP32 VALU forms are disabled for all device code of this library
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the leading kernel arguments (up to 16 dwords of pointers and scalars)
+    # arrive in SGPRs with the dispatch instead of by a load at wave start
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wno-unused-result", f"-I{INCLUDE}",
 ]
 

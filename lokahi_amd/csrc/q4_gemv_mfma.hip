@@ -115,13 +115,18 @@ constexpr int kGvWavesPerEu = MP != 0 ? 2 : (EPI == 2 ? 4 : 7);
 // 4 phases, so the block has twice the waves, each with half the chain.
 template <int MP, int EPI, bool NORM, typename YT, int NTC, int HT = 1>
 __global__ __launch_bounds__(NTC ? 64 * NTC * HT : (MP == 2 ? 512 : 1024)) __attribute__((amdgpu_waves_per_eu(kGvWavesPerEu<MP, EPI>)))
-void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
+void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, const uint4* __restrict__ codes,
+                         const uint4* __restrict__ sbp, const uint16_t* __restrict__ nw, int Ma,
+                         int K, int nta, GvArgs a) {
   static_assert(HT == 1 || (HT == 2 && MP == 0), "half tasks are batch-1 only");
   constexpr int MM = MP == 0 ? 1 : 4 * MP;  // staged batch rows (MP 2: 8)
   constexpr int NE = 2 / HT;           // x uint4 per lane of the wave's (half) task
   constexpr int NWL = 8 / HT;          // weight loads per lane
   extern __shared__ uint4 smem[];
-  const int nt = NTC ? NTC : a.nt, K = a.K;
+  // x, the weights, the norm weights and the shape lead the argument list:
+  // the dispatch preloads them into SGPRs, so the first loads issue without
+  // waiting for the argument segment.
+  const int nt = NTC ? NTC : nta;
   // a.pair (MP 1, 5-8 rows): workgroups 16 i + c and 16 i + 8 + c take batch
   // rows 0-3 and 4-7 of row block 8 i + c.  Both run on XCD c, one soon
   // after the other, so the second finds the block's weights in that L2.
@@ -134,14 +139,8 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, GvArgs a) {
       if (rb >= a.nrb) return;  // grid padding (whole workgroup)
     }
   }
-  const int M = MP == 1 ? min(4, a.M - ro) : a.M;  // rows of this workgroup
+  const int M = MP == 1 ? min(4, Ma - ro) : Ma;  // rows of this workgroup
   const uint16_t* const xp = x + (int64_t)ro * K;
-  // Every kernel argument the load issue below needs, in SGPRs at once: one
-  // wait for the argument loads instead of one per field between the loads.
-  const uint4* const codes = a.codes;
-  const uint4* const sbp = a.sb;
-  const uint16_t* const nw = NORM ? a.norm_w : nullptr;
-  asm volatile("" ::"s"(xp), "s"(codes), "s"(sbp), "s"(nw), "s"(M), "s"(K), "s"(nt));
   const int lane = threadIdx.x & 63, j = lane >> 4, n = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int t = HT == 2 ? wave >> 1 : wave;  // this wave's K task
@@ -561,7 +560,7 @@ void launch_one(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
   const size_t lds = (size_t)waves * (kWaveLds<MM> + MM * 64 + MM * 4);
   const int grid = a.pair ? 2 * ((nrb + 7) / 8 * 8) : nrb;
   hipLaunchKernelGGL((q4_gemv_mfma_kernel<MP, EPI, NORM, YT, NTC, HT>), dim3(grid), dim3(64 * waves),
-                     lds, st, x, a);
+                     lds, st, x, a.codes, a.sb, NORM ? a.norm_w : nullptr, a.M, a.K, a.nt, a);
 }
 
 template <int MP, int EPI, bool NORM, typename YT>
