@@ -112,12 +112,14 @@ struct Raw {
 // merge fetches them with wide loads in one round trip).
 constexpr int kMaxDecodeSplits = 256;
 
+// Everything the first K/V and q loads need leads the argument list (16
+// dwords, preloaded into SGPRs with the dispatch).
 template <typename TQ, typename TK, typename TV, int D, int G>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const TQ* __restrict__ q, const TK* __restrict__ k, const TV* __restrict__ v,
-    int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int Hq, int Hkv, int Lk,
-    const int* __restrict__ dlen, int causal, int chunk, int nsplit, float scale, float eps,
-    float* __restrict__ part, TQ* __restrict__ out, int gfull) {
+    int64_t kv_bs, int64_t kv_hs, int Lk, int chunk, int gfull, int Hq,
+    const int32_t* __restrict__ qpos, const int* __restrict__ dlen, int causal, int nsplit,
+    float scale, float eps, float* __restrict__ part, TQ* __restrict__ out) {
   constexpr int EPL = 16 / sizeof(TK);          // key elements per lane
   constexpr int LPK = D / EPL;                  // lanes per key
   constexpr int KPW = 64 / LPK;                 // keys per wave step
@@ -1310,8 +1312,8 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
 #define STRATA_DEC(GV)                                                                        \
   if (HG == GV)                                                                               \
     hipLaunchKernelGGL((attn_decode_kernel<TQ, TK, TV, D, GV>), grid, dim3(256), 0, stream,   \
-                       (const TQ*)q, (const TK*)k, (const TV*)v, kv_bs, kv_hs, qpos, Hq, Hkv, \
-                       Lk, ex.dlen, causal, chunk, nsplit, scale, eps, part, (TQ*)out, G);
+                       (const TQ*)q, (const TK*)k, (const TV*)v, kv_bs, kv_hs, Lk, chunk, G,  \
+                       Hq, qpos, ex.dlen, causal, nsplit, scale, eps, part, (TQ*)out);
   STRATA_DEC(1) else STRATA_DEC(2) else STRATA_DEC(3) else STRATA_DEC(4) else STRATA_DEC(6) else
   STRATA_DEC(8) else
     return strata_set_error(STRATA_ENOTSUP, "decode attention: group size %d not in {1,2,3,4,6,8}",
