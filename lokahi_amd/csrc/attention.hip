@@ -902,11 +902,12 @@ void attn_prefill_mfma32(
 // through a ring of NST stages private to the wave (direct global -> LDS
 // loads, no barrier).  Partials (m, s, o[D]) per head go to `part` for
 // attn_decode_merge, or the output is finalised when there is one chunk.
+// The arguments the first K/V loads need lead the list (16 preloaded dwords).
 template <int D, int NST, int WPG>
 __global__ __launch_bounds__(64 * WPG) void attn_decode_mfma(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-    int64_t kv_bs, int64_t kv_hs, const int32_t* __restrict__ qpos, int B, int Hq, int Hkv,
-    int Lk, const int* __restrict__ dlen, int causal, int chunk, int nsplit, float scale,
+    int64_t kv_bs, int64_t kv_hs, int B, int Hq, int Hkv, int Lk, int chunk, int nsplit,
+    const int32_t* __restrict__ qpos, const int* __restrict__ dlen, int causal, float scale,
     float eps, float* __restrict__ part, bf16_t* __restrict__ out) {
   constexpr int KT = 32;
   constexpr int ROW = D * 2;
@@ -1275,7 +1276,7 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
       const int items = B * Hkv * ns;
       hipLaunchKernelGGL((attn_decode_mfma<D, 2, WPG>), dim3((items + WPG - 1) / WPG), dim3(64 * WPG),
                          0, stream, (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, kv_bs,
-                         kv_hs, qpos, B, Hq, Hkv, Lk, ex.dlen, causal, ch, ns, scale, eps, pt,
+                         kv_hs, B, Hq, Hkv, Lk, ch, ns, qpos, ex.dlen, causal, scale, eps, pt,
                          (bf16_t*)out);
       STRATA_HIP_CHECK(hipGetLastError());
       if (ns > 1) {
