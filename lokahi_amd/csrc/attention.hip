@@ -383,6 +383,77 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict
   }
 }
 
+// grid (B*Hq), one wave: the same combination for D in {64, 128} and at
+// most NS splits.  Lane l holds split l's (m, s) and its weight; it reads
+// head-dim entries C*l .. C*l+C-1 of every split (all loads issued first)
+// and takes each split's weight by a constant-lane read.  No LDS, no barrier.
+template <typename TQ, int D, int NS>
+__global__ __launch_bounds__(64) void attn_decode_merge_w(const float* __restrict__ part,
+                                                          int nsplit, float eps,
+                                                          TQ* __restrict__ out) {
+  constexpr int C = D / 64;
+  const int bh = blockIdx.x, lane = threadIdx.x;
+  const float* pp = part + (int64_t)bh * part_stride(nsplit, D);
+  const float2* ms = reinterpret_cast<const float2*>(pp + (int64_t)nsplit * D);
+  float2 my = ms[min(lane, nsplit - 1)];
+  float ov[NS][C];
+#pragma unroll
+  for (int sp = 0; sp < NS; ++sp) {
+    const float* row = pp + (int64_t)min(sp, nsplit - 1) * D + C * lane;
+    if constexpr (C == 2) {
+      const float2 t = *reinterpret_cast<const float2*>(row);
+      ov[sp][0] = t.x;
+      ov[sp][1] = t.y;
+    } else {
+      ov[sp][0] = *row;
+    }
+  }
+  if (lane >= nsplit) my.y = 0.f;
+  const float mb = wave_max(my.y > 0.f ? my.x : -INFINITY);
+  const float mref = mb == -INFINITY ? 0.f : mb;
+  const float w = my.y > 0.f ? __builtin_amdgcn_exp2f(my.x - mref) : 0.f;  // 0 past nsplit
+  const float ss = wave_sum(my.y * w);
+  float acc[C] = {};
+#pragma unroll
+  for (int sp = 0; sp < NS; ++sp) {
+    const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), sp));
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[c] = fmaf(ov[sp][c], ws, acc[c]);
+  }
+  const float inv = 1.f / fmaxf(ss, eps);
+#pragma unroll
+  for (int c = 0; c < C; ++c) Elem<TQ>::store(out, (int64_t)bh * D + C * lane + c, acc[c] * inv);
+}
+
+// The merge launch for nsplit > 1 partials of B*Hq rows.
+template <typename TQ>
+void launch_decode_merge(const float* part, int nsplit, int D, int rows, float eps, TQ* out,
+                         hipStream_t st) {
+#define STRATA_MW(DD, NN)                                                                    \
+  hipLaunchKernelGGL((attn_decode_merge_w<TQ, DD, NN>), dim3(rows), dim3(64), 0, st, part,  \
+                     nsplit, eps, out)
+  // (NS in steps of 8 up to 48: the loads past nsplit repeat the last split)
+#define STRATA_MWD(DD)                                                  \
+  if (nsplit <= 16) STRATA_MW(DD, 16);                                  \
+  else if (nsplit <= 24) STRATA_MW(DD, 24);                             \
+  else if (nsplit <= 32) STRATA_MW(DD, 32);                             \
+  else if (nsplit <= 40) STRATA_MW(DD, 40);                             \
+  else if (nsplit <= 48) STRATA_MW(DD, 48);                             \
+  else STRATA_MW(DD, 64);
+  if ((D == 64 || D == 128) && nsplit <= 64) {
+    if (D == 128) {
+      STRATA_MWD(128)
+    } else {
+      STRATA_MWD(64)
+    }
+  } else {
+    hipLaunchKernelGGL((attn_decode_merge<TQ>), dim3(rows), dim3(256), 0, st, part, nsplit, D,
+                       eps, out);
+  }
+#undef STRATA_MWD
+#undef STRATA_MW
+}
+
 // ----------------------------------------------------------- prefill on MFMA
 // Workgroup wg of the prefill grid -> (query tile, b, kv head, query head).
 // remap: workgroups are dealt to the 8 XCDs round-robin (wg % 8); a group
@@ -1280,8 +1351,7 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
                          (bf16_t*)out);
       STRATA_HIP_CHECK(hipGetLastError());
       if (ns > 1) {
-        hipLaunchKernelGGL((attn_decode_merge<TQ>), dim3(B * Hq), dim3(256), 0, stream, pt, ns, D,
-                           eps, (TQ*)out);
+        launch_decode_merge<TQ>(pt, ns, D, B * Hq, eps, (TQ*)out, stream);
         STRATA_HIP_CHECK(hipGetLastError());
       }
       return STRATA_OK;
@@ -1322,8 +1392,7 @@ int launch_decode(strata_ctx* ctx, const void* q, const void* k, const void* v, 
 #undef STRATA_DEC
   STRATA_HIP_CHECK(hipGetLastError());
   if (nsplit > 1) {
-    hipLaunchKernelGGL((attn_decode_merge<TQ>), dim3(B * Hq), dim3(256), 0, stream, part, nsplit,
-                       D, eps, (TQ*)out);
+    launch_decode_merge<TQ>(part, nsplit, D, B * Hq, eps, (TQ*)out, stream);
     STRATA_HIP_CHECK(hipGetLastError());
   }
   return STRATA_OK;
