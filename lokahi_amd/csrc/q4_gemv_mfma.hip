@@ -108,18 +108,17 @@ template <int MP, int EPI>
 constexpr int kGvWavesPerEu = MP != 0 ? 2 : (EPI == 2 ? 4 : 7);
 
 // NTC: the K task count when known at compile time (4: the 8B hidden width,
-// 14: the 8B FFN width, 3 and 8: the 3B widths), 0 for any (up to 16; up to
-// 8 for the 8-row kernels, MP 2).
+// 14: the 8B FFN width, 3 and 8: the 3B widths), 0 for any (up to 16).
 // HT: waves per K task.  With HT = 2 (batch 1, launches too small to fill
 // the GPU) each wave takes half a task, 4 of its 8 weight loads and 2 of its
 // 4 phases, so the block has twice the waves, each with half the chain.
 template <int MP, int EPI, bool NORM, typename YT, int NTC, int HT = 1>
-__global__ __launch_bounds__(NTC ? 64 * NTC * HT : (MP == 2 ? 512 : 1024)) __attribute__((amdgpu_waves_per_eu(kGvWavesPerEu<MP, EPI>)))
+__global__ __launch_bounds__(NTC ? 64 * NTC * HT : 1024) __attribute__((amdgpu_waves_per_eu(kGvWavesPerEu<MP, EPI>)))
 void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, const uint4* __restrict__ codes,
                          const uint4* __restrict__ sbp, const uint16_t* __restrict__ nw, int Ma,
                          int K, int nta, GvArgs a) {
   static_assert(HT == 1 || (HT == 2 && MP == 0), "half tasks are batch-1 only");
-  constexpr int MM = MP == 0 ? 1 : 4 * MP;  // staged batch rows (MP 2: 8)
+  constexpr int MM = MP == 0 ? 1 : 4;  // staged batch rows
   constexpr int NE = 2 / HT;           // x uint4 per lane of the wave's (half) task
   constexpr int NWL = 8 / HT;          // weight loads per lane
   extern __shared__ uint4 smem[];
@@ -201,9 +200,7 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, const uint4* __restrict
   const int lb = rb - a.p[pi].rb0;
   const int em = threadIdx.x >> 4, er = threadIdx.x & 15;  // epilogue thread: batch row, block row
   const int eb = em + ro;  // its row of the whole batch
-  // (MP 2: batch rows 4..7 on the second wave; the host launches it with at
-  // least two waves)
-  const bool eth = (MP == 2 ? wave < 2 : wave == 0) && em < M;
+  const bool eth = wave == 0 && em < M;
   // epilogue operands, fetched now (they return with the weights); the
   // residual values are loaded by every lane at an in-bounds index
   uint16_t hpre = 0;
@@ -344,63 +341,40 @@ void q4_gemv_mfma_kernel(const uint16_t* __restrict__ x, const uint4* __restrict
       for (int i = 0; i < 4; ++i) red[wave * 16 + 4 * j + i] = acc[i];
     }
   } else {
-    // column n = 4 b + j': batch row b (+ 4 hf for the second accumulator
-    // set of MP 2, which shares every A operand), group 4 ph + j' of the phase
-    constexpr int NH = MM / 4;
+    // column n = 4 b + j': batch row b, group 4 ph + j' of the phase
     const int bm = n >> 2, jg = n & 3;
-    float accs[NH][4];
-#pragma unroll
-    for (int hf = 0; hf < NH; ++hf)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) accs[hf][i] = 0.f;
+    const bool act = jg == j && bm < M;
 #pragma unroll
     for (int ph = 0; ph < 4; ++ph) {
-      const uint4* bb[NH];
-#pragma unroll
-      for (int hf = 0; hf < NH; ++hf)
-        bb[hf] = jg == j && 4 * hf + bm < M ? xw + (4 * hf + bm) * 128 + (4 * ph + j) * 8 : zero;
-      f32x4_t c0[NH], c1[NH];
-#pragma unroll
-      for (int hf = 0; hf < NH; ++hf) {
-        c0[hf] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        c1[hf] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      }
+      const uint4* bb = act ? xw + bm * 128 + (4 * ph + j) * 8 : zero;
+      f32x4_t c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int o = 0; o < 8; ++o) {
         const u32x4_t av = a_op(8 * ph + o);
-#pragma unroll
-        for (int hf = 0; hf < NH; ++hf) {
-          const uint4 bv = bb[hf][o];
-          const u32x4_t bq = {bv.x, bv.y, bv.z, bv.w};
-          if (o & 1) c1[hf] = mfma16(av, bq, c1[hf]);
-          else c0[hf] = mfma16(av, bq, c0[hf]);
-        }
+        const uint4 bv = bb[o];
+        const u32x4_t bq = {bv.x, bv.y, bv.z, bv.w};
+        if (o & 1) c1 = mfma16(av, bq, c1);
+        else c0 = mfma16(av, bq, c0);
       }
+      const float X = xs[min(bm, MM - 1) * 16 + 4 * ph + jg];
       const uint32_t sw[4] = {sbv[ph].x, sbv[ph].y, sbv[ph].z, sbv[ph].w};
 #pragma unroll
-      for (int hf = 0; hf < NH; ++hf) {
-        const float X = xs[min(4 * hf + bm, MM - 1) * 16 + 4 * ph + jg];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float sc = __uint_as_float(sw[i] << 16), bc = __uint_as_float(sw[i] & 0xffff0000u);
-          accs[hf][i] += sc * (c0[hf][i] + c1[hf][i]) + fmaf(-128.f, sc, bc) * X;
-        }
+      for (int i = 0; i < 4; ++i) {
+        const float sc = __uint_as_float(sw[i] << 16), bc = __uint_as_float(sw[i] & 0xffff0000u);
+        acc[i] += sc * (c0[i] + c1[i]) + fmaf(-128.f, sc, bc) * X;
       }
     }
     // sum the 4 group columns of each batch row (one lane quad)
 #pragma unroll
-    for (int hf = 0; hf < NH; ++hf) {
+    for (int i = 0; i < 4; ++i) {
+      float v = acc[i];
+      v += dppv<0xB1>(v);
+      v += dppv<0x4E>(v);
+      acc[i] = v;
+    }
+    if (jg == 0 && bm < M) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float v = accs[hf][i];
-        v += dppv<0xB1>(v);
-        v += dppv<0x4E>(v);
-        accs[hf][i] = v;
-      }
-      if (jg == 0 && 4 * hf + bm < M) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) red[(wave * MM + 4 * hf + bm) * 16 + 4 * j + i] = accs[hf][i];
-      }
+      for (int i = 0; i < 4; ++i) red[(wave * MM + bm) * 16 + 4 * j + i] = acc[i];
     }
   }
   __syncthreads();
@@ -555,7 +529,7 @@ constexpr int64_t kGvHalfTaskWaves = 4096;
 
 template <int MP, int EPI, bool NORM, typename YT, int NTC, int HT>
 void launch_one(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
-  constexpr int MM = MP == 0 ? 1 : 4 * MP;
+  constexpr int MM = MP == 0 ? 1 : 4;
   const int waves = a.nt * HT;
   const size_t lds = (size_t)waves * (kWaveLds<MM> + MM * 64 + MM * 4);
   const int grid = a.pair ? 2 * ((nrb + 7) / 8 * 8) : nrb;
@@ -571,11 +545,9 @@ void launch_gv(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
     else launch_one<MP, EPI, NORM, YT, 4, 1>(x, a, nrb, st);
     return;
   }
-  if constexpr (MP != 2) {  // (8 staged rows of 14 tasks exceed the LDS)
-    if (a.nt == 14 && !NORM) {
-      launch_one<MP, EPI, NORM, YT, 14, 1>(x, a, nrb, st);
-      return;
-    }
+  if (a.nt == 14 && !NORM) {
+    launch_one<MP, EPI, NORM, YT, 14, 1>(x, a, nrb, st);
+    return;
   }
   // the 3B widths (3072, and 8192 for down); the batched kernels need the
   // small block's register budget too (the generic 1024-thread bound spills)
@@ -598,9 +570,7 @@ void launch_gv_m(const uint16_t* x, const GvArgs& a, int nrb, hipStream_t st) {
     launch_gv<0, EPI, NORM, YT>(x, a, nrb, st);
   } else if (a.M <= 4) {
     launch_gv<1, EPI, NORM, YT>(x, a, nrb, st);
-  } else if (gv_eight_rows(a.K)) {
-    launch_gv<2, EPI, NORM, YT>(x, a, nrb, st);
-  } else {  // 8 staged rows would not fit the LDS: paired 4-row workgroups
+  } else {  // 5-8 rows: paired 4-row workgroups
     GvArgs b = a;
     b.pair = 1;
     launch_gv<1, EPI, NORM, YT>(x, b, nrb, st);

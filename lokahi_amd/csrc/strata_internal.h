@@ -41,12 +41,9 @@ struct GemvLayout {
   int rb0[kGvMaxProblems + 1] = {};  // first row block of each problem
   int64_t N[kGvMaxProblems] = {};     // output rows of each problem
 };
-// Batch rows of one layout launch: up to kGvMaxRows.  5-8 rows run as one
-// 8-row workgroup per row block where its 8 staged x rows fit the LDS and its
-// epilogue has two waves (gv_eight_rows: two to eight 1024-wide K tasks),
-// else as two 4-row workgroups per row block in one grid.
+// Batch rows of one layout launch: up to kGvMaxRows (5-8 rows run as two
+// 4-row workgroups per row block in one grid).
 constexpr int kGvMaxRows = 8;
-inline bool gv_eight_rows(int K) { return K > 1024 && K <= 8192; }
 // K % 64 == 0, K <= 16384 and 1 <= M <= 8.
 bool strata_gemv_layout_fits(int K, int M);
 int strata_gemv_layout_build(const strata_q4_weight* ws, int count, int K, int perm, int head_dim,
