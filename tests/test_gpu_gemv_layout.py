@@ -62,11 +62,9 @@ def test_layout_gemv_batches_ragged_rows_padded_k(dev, M):
 @pytest.mark.parametrize("M,K", [(5, 1088), (8, 3072), (6, 4096), (7, 8192), (8, 4096),
                                  (8, 1024), (5, 14336), (8, 14336), (6, 16384)])
 def test_layout_gemv_eight_rows_equal_two_four_row_calls(dev, M, K):
-    """5..8 rows run in one launch.  For 1024 < K <= 8192 one workgroup per
-    row block feeds two 4-row accumulator sets from the same A operands;
-    otherwise two 4-row workgroups per row block share the grid.  Either way
-    every row is bit-identical to the same row in a 4-row call, and within
-    the fp32 tolerance of the oracle."""
+    """5..8 rows run in one launch: two 4-row workgroups per row block share
+    the grid.  Every row is bit-identical to the same row in a 4-row call,
+    and within the fp32 tolerance of the oracle."""
     rng = np.random.default_rng(50 + M + K)
     probs = [_weights(rng, n, K) for n in (100, 36, 17)]
     lay = _layout(dev, probs)
